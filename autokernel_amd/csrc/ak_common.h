@@ -1,0 +1,141 @@
+// ak_common.h -- shared device helpers for the gfx950 kernels of libak355.
+//
+// Element types are carried as traits (TF32 / TF16 / TBF16): storage type, elements per
+// 16-byte vector, and conversions to / from fp32. Rounding to f16 / bf16 is round-to-nearest-even
+// and overflows to +-inf (never clamps), which is what a torch tensor op does when it stores an
+// fp32 result into a half / bfloat16 tensor.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "../../include/ak355.h"
+
+namespace ak {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------------------------
+// Element-type traits
+// ---------------------------------------------------------------------------------------------
+struct TF32 {
+  using S = float;
+  static constexpr int kVec = 4;  // elements per 16-byte vector
+  static constexpr int kCode = AK_F32;
+  __device__ __forceinline__ static float to_f(S v) { return v; }
+  __device__ __forceinline__ static S from_f(float f) { return f; }
+  __device__ __forceinline__ static float rnd(float f) { return f; }
+  // i-th element of a 16-byte vector
+  __device__ __forceinline__ static float lane_elem(const u32x4& v, int i) {
+    return __uint_as_float(v[i]);
+  }
+  __device__ __forceinline__ static void set_elem(u32x4& v, int i, float f) { v[i] = __float_as_uint(f); }
+};
+
+struct TF16 {
+  using S = uint16_t;
+  static constexpr int kVec = 8;
+  static constexpr int kCode = AK_F16;
+  __device__ __forceinline__ static float to_f(S v) { return (float)__builtin_bit_cast(_Float16, v); }
+  __device__ __forceinline__ static S from_f(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+  __device__ __forceinline__ static float rnd(float f) { return (float)(_Float16)f; }
+  __device__ __forceinline__ static float lane_elem(const u32x4& v, int i) {
+    uint32_t w = v[i >> 1];
+    return to_f((S)((i & 1) ? (w >> 16) : (w & 0xffffu)));
+  }
+  __device__ __forceinline__ static void set_elem(u32x4& v, int i, float f) {
+    uint32_t h = from_f(f);
+    uint32_t w = v[i >> 1];
+    v[i >> 1] = (i & 1) ? ((w & 0xffffu) | (h << 16)) : ((w & 0xffff0000u) | h);
+  }
+};
+
+struct TBF16 {
+  using S = uint16_t;
+  static constexpr int kVec = 8;
+  static constexpr int kCode = AK_BF16;
+  __device__ __forceinline__ static float to_f(S v) { return __uint_as_float(((uint32_t)v) << 16); }
+  __device__ __forceinline__ static S from_f(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+  __device__ __forceinline__ static float rnd(float f) { return to_f(from_f(f)); }
+  __device__ __forceinline__ static float lane_elem(const u32x4& v, int i) {
+    uint32_t w = v[i >> 1];
+    return (i & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+  }
+  __device__ __forceinline__ static void set_elem(u32x4& v, int i, float f) {
+    uint32_t h = from_f(f);
+    uint32_t w = v[i >> 1];
+    v[i >> 1] = (i & 1) ? ((w & 0xffffu) | (h << 16)) : ((w & 0xffff0000u) | h);
+  }
+};
+
+// ---------------------------------------------------------------------------------------------
+// Memory helpers
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+// Streaming variants: data touched once, keep it out of the way of reused data.
+__device__ __forceinline__ u32x4 ld16_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ void st16_stream(void* p, const u32x4& v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
+// ---------------------------------------------------------------------------------------------
+// Wave64 butterfly reductions. The xor pattern fixes the combination order, so results are
+// bitwise reproducible run to run.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+// NaN-propagating max (torch.max semantics): any NaN operand gives NaN.
+__device__ __forceinline__ float nan_max(float a, float b) {
+  return (a != a || a > b) ? a : b;
+}
+__device__ __forceinline__ float wave_nan_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = nan_max(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+__device__ __forceinline__ bool aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
+
+// ---------------------------------------------------------------------------------------------
+// Host-side helpers
+// ---------------------------------------------------------------------------------------------
+int record_launch(void);  // checks hipGetLastError(), stores its text, returns AK_OK / AK_EHIP
+
+inline bool host_aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace ak
+
+// Dispatch an element-type code to a traits type: AK_DISPATCH(dtype, T, { body using T; })
+#define AK_DISPATCH(code, T, ...)                         \
+  switch (code) {                                         \
+    case AK_F32: { using T = ::ak::TF32; __VA_ARGS__; break; }   \
+    case AK_F16: { using T = ::ak::TF16; __VA_ARGS__; break; }   \
+    case AK_BF16: { using T = ::ak::TBF16; __VA_ARGS__; break; } \
+    default: return AK_EINVAL;                            \
+  }

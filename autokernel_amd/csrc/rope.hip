@@ -1,0 +1,120 @@
+// rope.hip -- interleaved rotary position embedding (reference.py:63-69) on gfx950.
+//
+// Pairs (x[2i], x[2i+1]) of each row rotate by table entry i of the row's position:
+//   y[2i]   = rnd(rnd(x[2i]*cos[i]) - rnd(x[2i+1]*sin[i]))
+//   y[2i+1] = rnd(rnd(x[2i]*sin[i]) + rnd(x[2i+1]*cos[i]))
+// rnd() rounds to the element type, as each elementwise tensor op of the reference does; for
+// fp32 no fused multiply-add is formed, so every element is bit-identical to the tensor ops.
+// The fast path moves one 16-byte vector of x (4 pairs for f16 / bf16) and two 8-byte table
+// slices per thread; the table rows stay hot in L2 across heads.
+#include <limits.h>
+
+#include "ak_common.h"
+
+namespace ak {
+
+#pragma clang fp contract(off)
+template <typename T>
+__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float* y1, float* y2) {
+  *y1 = T::rnd(T::rnd(x1 * c) - T::rnd(x2 * s));
+  *y2 = T::rnd(T::rnd(x1 * s) + T::rnd(x2 * c));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rope_vec(const typename T::S* __restrict__ x,
+                                                const typename T::S* __restrict__ ct,
+                                                const typename T::S* __restrict__ st,
+                                                typename T::S* __restrict__ y, int64_t nchunks,
+                                                int chunks_per_row, int half, int64_t table_rows,
+                                                int64_t rep_inner) {
+  using S = typename T::S;
+  constexpr int kP = T::kVec / 2;  // pairs per 16-byte vector
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nchunks) return;
+  const int64_t row = i / chunks_per_row;
+  const int c = (int)(i - row * chunks_per_row);
+  const int64_t trow = (row / rep_inner) % table_rows;
+  const u32x4 xv = ld16(x + i * T::kVec);
+  const S* cp = ct + trow * half + c * kP;
+  const S* sp = st + trow * half + c * kP;
+  float cf[kP], sf[kP];
+  if constexpr (kP == 4) {  // 2-byte types: 8 bytes of cos, 8 bytes of sin
+    const u32x2 cv = *reinterpret_cast<const u32x2*>(cp);
+    const u32x2 sv = *reinterpret_cast<const u32x2*>(sp);
+    const u32x4 c4 = {cv[0], cv[1], 0u, 0u}, s4 = {sv[0], sv[1], 0u, 0u};
+#pragma unroll
+    for (int p = 0; p < kP; ++p) {
+      cf[p] = T::lane_elem(c4, p);
+      sf[p] = T::lane_elem(s4, p);
+    }
+  } else {  // fp32: 2 pairs per vector
+#pragma unroll
+    for (int p = 0; p < kP; ++p) {
+      cf[p] = T::to_f(cp[p]);
+      sf[p] = T::to_f(sp[p]);
+    }
+  }
+  u32x4 yv;
+#pragma unroll
+  for (int p = 0; p < kP; ++p) {
+    float y1, y2;
+    rope_pair<T>(T::lane_elem(xv, 2 * p), T::lane_elem(xv, 2 * p + 1), cf[p], sf[p], &y1, &y2);
+    T::set_elem(yv, 2 * p, y1);
+    T::set_elem(yv, 2 * p + 1, y2);
+  }
+  st16(y + i * T::kVec, yv);
+}
+
+// Any alignment: one pair per thread.
+template <typename T>
+__global__ __launch_bounds__(256) void rope_scalar(const typename T::S* __restrict__ x,
+                                                   const typename T::S* __restrict__ ct,
+                                                   const typename T::S* __restrict__ st,
+                                                   typename T::S* __restrict__ y, int64_t npairs,
+                                                   int half, int64_t table_rows, int64_t rep_inner) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= npairs) return;
+  const int64_t row = i / half;
+  const int p = (int)(i - row * half);
+  const int64_t trow = (row / rep_inner) % table_rows;
+  float y1, y2;
+  rope_pair<T>(T::to_f(x[2 * i]), T::to_f(x[2 * i + 1]), T::to_f(ct[trow * half + p]),
+               T::to_f(st[trow * half + p]), &y1, &y2);
+  y[2 * i] = T::from_f(y1);
+  y[2 * i + 1] = T::from_f(y2);
+}
+#pragma clang fp contract(on)
+
+template <typename T>
+static int launch_rope(const void* x, const void* c, const void* s, void* y, int64_t rows,
+                       int64_t d, int64_t table_rows, int64_t rep_inner, hipStream_t stream) {
+  using S = typename T::S;
+  const int half = (int)(d / 2);
+  const bool vec = d % T::kVec == 0 && host_aligned16(x) && host_aligned16(y) &&
+                   (((uintptr_t)c | (uintptr_t)s) & 7u) == 0;
+  if (vec) {
+    const int cpr = (int)(d / T::kVec);
+    const int64_t n = rows * cpr;
+    rope_vec<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>((const S*)x, (const S*)c, (const S*)s,
+                                                            (S*)y, n, cpr, half, table_rows, rep_inner);
+  } else {
+    const int64_t n = rows * half;
+    rope_scalar<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>((const S*)x, (const S*)c, (const S*)s,
+                                                               (S*)y, n, half, table_rows, rep_inner);
+  }
+  return record_launch();
+}
+
+}  // namespace ak
+
+using namespace ak;
+
+extern "C" int ak_rope(int dtype, const void* x, const void* cos_t, const void* sin_t, void* y,
+                       int64_t rows, int64_t head_dim, int64_t table_rows, int64_t rep_inner,
+                       hipStream_t stream) {
+  if (rows < 0 || head_dim < 0 || head_dim % 2 != 0 || head_dim > INT_MAX) return AK_EINVAL;
+  if (rows == 0 || head_dim == 0) return AK_OK;
+  if (!x || !cos_t || !sin_t || !y || table_rows <= 0 || rep_inner <= 0) return AK_EINVAL;
+  if (rows * head_dim / 2 > (int64_t)UINT_MAX * 256) return AK_EINVAL;
+  AK_DISPATCH(dtype, T, return launch_rope<T>(x, cos_t, sin_t, y, rows, head_dim, table_rows, rep_inner, stream));
+}

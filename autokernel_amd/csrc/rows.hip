@@ -1,0 +1,546 @@
+// rows.hip -- row-parallel ops on gfx950: rmsnorm, layernorm, softmax, cross_entropy and the
+// last-dim reductions. All are HBM-bound: each row is read once into registers (row_common.h)
+// and written once; reductions are wave64 butterflies plus a fixed-order LDS combine.
+#include <limits.h>
+
+#include "row_common.h"
+
+namespace ak {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kLoopThreads = 256;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Every wave of a 256-thread block calls this; kind as in group_combine.
+template <int KIND>
+__device__ __forceinline__ float block_reduce(float v, float* red) {
+  return group_reduce<kLoopThreads, KIND>(v, red);
+}
+
+// =============================================================================================
+// RMSNorm. Op sequence of reference.py:28-29, each a tensor op in x's dtype:
+//   sq = x**2; ms = mean(sq); t = ms + eps; rms = sqrt(t); q = x / rms; y = q * weight
+// so x*x rounds (and may overflow to inf) in f16 before the fp32-accumulated mean.
+// =============================================================================================
+template <typename T>
+struct RmsStats {
+  __device__ __forceinline__ static float inv_rms(float ss, int cols, float eps) {
+    const float ms = T::rnd(ss / (float)cols);
+    const float rms = T::rnd(sqrtf(T::rnd(ms + eps)));
+    return 1.0f / rms;  // x / rms == x * (1 / rms) to within one fp32 ulp before rounding
+  }
+};
+
+template <typename T, int L, int VPT>
+__global__ __launch_bounds__(RowGeom<L>::kThreads) void rmsnorm_rows(
+    const typename T::S* __restrict__ x, const typename T::S* __restrict__ w,
+    typename T::S* __restrict__ y, int64_t rows, int cols, float eps) {
+  using G = RowGeom<L>;
+  __shared__ float red[G::kWPB];
+  const int gl = G::lane_in_row();
+  const int64_t row = (int64_t)blockIdx.x * G::kRowsPerBlock + G::group();
+  const bool active = row < rows;
+  const int nvec = active ? cols / T::kVec : 0;
+  RowRegs<T, L, VPT> r;
+  r.load(x + row * cols, nvec, gl);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < RowRegs<T, L, VPT>::kE; ++e) ss += T::rnd(r.f[e] * r.f[e]);
+  ss = group_reduce<L, 0>(ss, red);
+  const float inv = RmsStats<T>::inv_rms(ss, cols, eps);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int idx = gl + j * L;
+    if (idx < nvec) {
+      const u32x4 wv = ld16(w + (int64_t)idx * T::kVec);
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < T::kVec; ++e)
+        T::set_elem(o, e, T::rnd(r.f[j * T::kVec + e] * inv) * T::lane_elem(wv, e));
+      st16(y + row * cols + (int64_t)idx * T::kVec, o);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kLoopThreads) void rmsnorm_loop(
+    const typename T::S* __restrict__ x, const typename T::S* __restrict__ w,
+    typename T::S* __restrict__ y, int cols, float eps) {
+  __shared__ float red[kLoopThreads / kWave];
+  const typename T::S* xr = x + (int64_t)blockIdx.x * cols;
+  typename T::S* yr = y + (int64_t)blockIdx.x * cols;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < cols; c += kLoopThreads) {
+    const float v = T::to_f(xr[c]);
+    ss += T::rnd(v * v);
+  }
+  ss = block_reduce<0>(ss, red);
+  const float inv = RmsStats<T>::inv_rms(ss, cols, eps);
+  for (int c = threadIdx.x; c < cols; c += kLoopThreads)
+    yr[c] = T::from_f(T::rnd(T::to_f(xr[c]) * inv) * T::to_f(w[c]));
+}
+
+template <typename T>
+static int launch_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int64_t cols,
+                          float eps, hipStream_t s) {
+  using S = typename T::S;
+  const S* xp = (const S*)x;
+  const S* wp = (const S*)w;
+  S* yp = (S*)y;
+  RowPlan plan;
+  const bool vec = cols % T::kVec == 0 && host_aligned16(x) && host_aligned16(y) && host_aligned16(w);
+  bool handled = false;
+  if (vec && plan_row(cols / T::kVec, T::kVec, &plan)) {
+    AK_ROW_SWITCH({
+      const dim3 grid((unsigned)cdiv(rows, RowGeom<L>::kRowsPerBlock));
+      rmsnorm_rows<T, L, VPT><<<grid, RowGeom<L>::kThreads, 0, s>>>(xp, wp, yp, rows, (int)cols, eps);
+    });
+  }
+  if (!handled) rmsnorm_loop<T><<<(unsigned)rows, kLoopThreads, 0, s>>>(xp, wp, yp, (int)cols, eps);
+  return record_launch();
+}
+
+// =============================================================================================
+// LayerNorm: F.layer_norm over the last dim (reference.py:20-23): fp32 mean and biased variance,
+// rstd = rsqrt(var + eps), y = (x - mean) * rstd * w + b rounded once.
+// =============================================================================================
+template <typename T>
+__device__ __forceinline__ float ln_out(float v, float mean, float rstd, const typename T::S* w,
+                                        const typename T::S* b, int64_t c) {
+  float o = (v - mean) * rstd;
+  if (w) o *= T::to_f(w[c]);
+  if (b) o += T::to_f(b[c]);
+  return o;
+}
+
+template <typename T, int L, int VPT>
+__global__ __launch_bounds__(RowGeom<L>::kThreads) void layernorm_rows(
+    const typename T::S* __restrict__ x, const typename T::S* __restrict__ w,
+    const typename T::S* __restrict__ b, typename T::S* __restrict__ y, int64_t rows, int cols,
+    float eps) {
+  using G = RowGeom<L>;
+  using R = RowRegs<T, L, VPT>;
+  __shared__ float red[G::kWPB];
+  const int gl = G::lane_in_row();
+  const int64_t row = (int64_t)blockIdx.x * G::kRowsPerBlock + G::group();
+  const bool active = row < rows;
+  const int nvec = active ? cols / T::kVec : 0;
+  R r;
+  r.load(x + row * cols, nvec, gl);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < R::kE; ++e) s += r.f[e];  // invalid vectors hold 0
+  const float mean = group_reduce<L, 0>(s, red) / (float)cols;
+  float d = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    if (R::valid(j, gl, nvec)) {
+#pragma unroll
+      for (int e = 0; e < T::kVec; ++e) {
+        const float t = r.f[j * T::kVec + e] - mean;
+        d += t * t;
+      }
+    }
+  }
+  const float var = group_reduce<L, 0>(d, red) / (float)cols;
+  const float rstd = rsqrtf(var + eps);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int idx = gl + j * L;
+    if (idx < nvec) {
+      u32x4 wv = {0u, 0u, 0u, 0u}, bv = {0u, 0u, 0u, 0u};
+      if (w) wv = ld16(w + (int64_t)idx * T::kVec);
+      if (b) bv = ld16(b + (int64_t)idx * T::kVec);
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < T::kVec; ++e) {
+        float v = (r.f[j * T::kVec + e] - mean) * rstd;
+        if (w) v *= T::lane_elem(wv, e);
+        if (b) v += T::lane_elem(bv, e);
+        T::set_elem(o, e, v);
+      }
+      st16(y + row * cols + (int64_t)idx * T::kVec, o);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kLoopThreads) void layernorm_loop(
+    const typename T::S* __restrict__ x, const typename T::S* __restrict__ w,
+    const typename T::S* __restrict__ b, typename T::S* __restrict__ y, int cols, float eps) {
+  __shared__ float red[kLoopThreads / kWave];
+  const typename T::S* xr = x + (int64_t)blockIdx.x * cols;
+  typename T::S* yr = y + (int64_t)blockIdx.x * cols;
+  float s = 0.f;
+  for (int c = threadIdx.x; c < cols; c += kLoopThreads) s += T::to_f(xr[c]);
+  const float mean = block_reduce<0>(s, red) / (float)cols;
+  float d = 0.f;
+  for (int c = threadIdx.x; c < cols; c += kLoopThreads) {
+    const float t = T::to_f(xr[c]) - mean;
+    d += t * t;
+  }
+  const float rstd = rsqrtf(block_reduce<0>(d, red) / (float)cols + eps);
+  for (int c = threadIdx.x; c < cols; c += kLoopThreads)
+    yr[c] = T::from_f(ln_out<T>(T::to_f(xr[c]), mean, rstd, w, b, c));
+}
+
+template <typename T>
+static int launch_layernorm(const void* x, const void* w, const void* b, void* y, int64_t rows,
+                            int64_t cols, float eps, hipStream_t s) {
+  using S = typename T::S;
+  const S* xp = (const S*)x;
+  const S* wp = (const S*)w;
+  const S* bp = (const S*)b;
+  S* yp = (S*)y;
+  RowPlan plan;
+  const bool vec = cols % T::kVec == 0 && host_aligned16(x) && host_aligned16(y) &&
+                   (!w || host_aligned16(w)) && (!b || host_aligned16(b));
+  bool handled = false;
+  if (vec && plan_row(cols / T::kVec, T::kVec, &plan)) {
+    AK_ROW_SWITCH({
+      const dim3 grid((unsigned)cdiv(rows, RowGeom<L>::kRowsPerBlock));
+      layernorm_rows<T, L, VPT><<<grid, RowGeom<L>::kThreads, 0, s>>>(xp, wp, bp, yp, rows, (int)cols, eps);
+    });
+  }
+  if (!handled) layernorm_loop<T><<<(unsigned)rows, kLoopThreads, 0, s>>>(xp, wp, bp, yp, (int)cols, eps);
+  return record_launch();
+}
+
+// =============================================================================================
+// Softmax over the last dim (reference.py:15-17): fp32 max, exp and sum, one rounding.
+// =============================================================================================
+template <typename T, int L, int VPT>
+__global__ __launch_bounds__(RowGeom<L>::kThreads) void softmax_rows(
+    const typename T::S* __restrict__ x, typename T::S* __restrict__ y, int64_t rows, int cols) {
+  using G = RowGeom<L>;
+  using R = RowRegs<T, L, VPT>;
+  __shared__ float red[G::kWPB];
+  const int gl = G::lane_in_row();
+  const int64_t row = (int64_t)blockIdx.x * G::kRowsPerBlock + G::group();
+  const bool active = row < rows;
+  const int nvec = active ? cols / T::kVec : 0;
+  R r;
+  r.load(x + row * cols, nvec, gl);
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j)
+    if (R::valid(j, gl, nvec))
+#pragma unroll
+      for (int e = 0; e < T::kVec; ++e) m = fmaxf(m, r.f[j * T::kVec + e]);
+  m = group_reduce<L, 1>(m, red);
+  const float mb = m * kLog2e;
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    if (R::valid(j, gl, nvec)) {
+#pragma unroll
+      for (int e = 0; e < T::kVec; ++e) {
+        const float p = fast_exp2(__builtin_fmaf(r.f[j * T::kVec + e], kLog2e, -mb));
+        r.f[j * T::kVec + e] = p;
+        s += p;
+      }
+    }
+  }
+  s = group_reduce<L, 0>(s, red);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int e = 0; e < R::kE; ++e) r.f[e] *= inv;
+  r.store(y + row * cols, nvec, gl);
+}
+
+// Online (max, sum-of-exp) accumulator used by the looped softmax and cross-entropy kernels.
+// -inf entries contribute nothing, +inf or NaN entries make the sum NaN (torch's softmax result).
+struct OnlineMS {
+  float m = -INFINITY;
+  float s = 0.f;
+  bool nan = false;
+  __device__ __forceinline__ void add(float v) {
+    if (v != v) { nan = true; return; }
+    const float mn = fmaxf(m, v);
+    if (mn == -INFINITY) return;
+    s = s * fast_exp2((m - mn) * kLog2e) + fast_exp2((v - mn) * kLog2e);
+    m = mn;
+  }
+};
+
+// Combine per-thread (m, s) over a 256-thread block in fixed order; returns the row's (M, S).
+__device__ __forceinline__ void block_combine_ms(OnlineMS a, float* red, float* M, float* S) {
+  float mx = block_reduce<1>(a.m, red);
+  float sc = (a.m == -INFINITY) ? 0.f : a.s * fast_exp2((a.m - mx) * kLog2e);
+  if (a.nan) sc = NAN;
+  float tot = block_reduce<0>(sc, red);
+  *M = mx;
+  *S = tot;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kLoopThreads) void softmax_loop(
+    const typename T::S* __restrict__ x, typename T::S* __restrict__ y, int cols) {
+  __shared__ float red[kLoopThreads / kWave];
+  const typename T::S* xr = x + (int64_t)blockIdx.x * cols;
+  typename T::S* yr = y + (int64_t)blockIdx.x * cols;
+  OnlineMS a;
+  for (int c = threadIdx.x; c < cols; c += kLoopThreads) a.add(T::to_f(xr[c]));
+  float M, S;
+  block_combine_ms(a, red, &M, &S);
+  const float inv = 1.0f / S;
+  const float mb = M * kLog2e;
+  for (int c = threadIdx.x; c < cols; c += kLoopThreads)
+    yr[c] = T::from_f(fast_exp2(__builtin_fmaf(T::to_f(xr[c]), kLog2e, -mb)) * inv);
+}
+
+template <typename T>
+static int launch_softmax(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t s) {
+  using S = typename T::S;
+  const S* xp = (const S*)x;
+  S* yp = (S*)y;
+  RowPlan plan;
+  const bool vec = cols % T::kVec == 0 && host_aligned16(x) && host_aligned16(y);
+  bool handled = false;
+  if (vec && plan_row(cols / T::kVec, T::kVec, &plan)) {
+    AK_ROW_SWITCH({
+      const dim3 grid((unsigned)cdiv(rows, RowGeom<L>::kRowsPerBlock));
+      softmax_rows<T, L, VPT><<<grid, RowGeom<L>::kThreads, 0, s>>>(xp, yp, rows, (int)cols);
+    });
+  }
+  if (!handled) softmax_loop<T><<<(unsigned)rows, kLoopThreads, 0, s>>>(xp, yp, (int)cols);
+  return record_launch();
+}
+
+// =============================================================================================
+// Cross entropy (reference.py:58-60 = F.cross_entropy, mean reduction, ignore_index):
+//   log_softmax in fp32 rounded to the logits' dtype, nll = -logp[target], then the mean of the
+//   rounded values accumulated in fp32 and rounded once. Per-row losses go to a caller-owned
+//   fp32 workspace; a single-block kernel then reduces them in a fixed order.
+// =============================================================================================
+template <typename T>
+__device__ __forceinline__ float ce_row_loss(const typename T::S* xr, int64_t t, int64_t vocab,
+                                             int64_t ignore_index, float M, float S) {
+  if (t == ignore_index) return 0.f;
+  if (t < 0 || t >= vocab) return NAN;
+  const float lp = T::rnd(T::to_f(xr[t]) - M - logf(S));
+  return -lp;
+}
+
+template <typename T, int L, int VPT>
+__global__ __launch_bounds__(RowGeom<L>::kThreads) void ce_rows(
+    const typename T::S* __restrict__ x, const int64_t* __restrict__ tgt, float* __restrict__ loss,
+    int64_t rows, int cols, int64_t ignore_index) {
+  using G = RowGeom<L>;
+  using R = RowRegs<T, L, VPT>;
+  __shared__ float red[G::kWPB];
+  const int gl = G::lane_in_row();
+  const int64_t row = (int64_t)blockIdx.x * G::kRowsPerBlock + G::group();
+  const bool active = row < rows;
+  const int nvec = active ? cols / T::kVec : 0;
+  R r;
+  r.load(x + row * cols, nvec, gl);
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j)
+    if (R::valid(j, gl, nvec))
+#pragma unroll
+      for (int e = 0; e < T::kVec; ++e) m = fmaxf(m, r.f[j * T::kVec + e]);
+  m = group_reduce<L, 1>(m, red);
+  const float mb = m * kLog2e;
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j)
+    if (R::valid(j, gl, nvec))
+#pragma unroll
+      for (int e = 0; e < T::kVec; ++e) s += fast_exp2(__builtin_fmaf(r.f[j * T::kVec + e], kLog2e, -mb));
+  s = group_reduce<L, 0>(s, red);
+  if (active && gl == 0) loss[row] = ce_row_loss<T>(x + row * cols, tgt[row], cols, ignore_index, m, s);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kLoopThreads) void ce_loop(
+    const typename T::S* __restrict__ x, const int64_t* __restrict__ tgt, float* __restrict__ loss,
+    int cols, int64_t ignore_index) {
+  __shared__ float red[kLoopThreads / kWave];
+  const typename T::S* xr = x + (int64_t)blockIdx.x * cols;
+  OnlineMS a;
+  for (int c = threadIdx.x; c < cols; c += kLoopThreads) a.add(T::to_f(xr[c]));
+  float M, S;
+  block_combine_ms(a, red, &M, &S);
+  if (threadIdx.x == 0) loss[blockIdx.x] = ce_row_loss<T>(xr, tgt[blockIdx.x], cols, ignore_index, M, S);
+}
+
+constexpr int kMeanThreads = 1024;
+
+template <typename T>
+__global__ __launch_bounds__(kMeanThreads) void ce_mean(const float* __restrict__ loss,
+                                                        const int64_t* __restrict__ tgt,
+                                                        typename T::S* __restrict__ out,
+                                                        int64_t rows, int64_t ignore_index) {
+  __shared__ float red[kMeanThreads / kWave];
+  float s = 0.f, n = 0.f;
+  for (int64_t r = threadIdx.x; r < rows; r += kMeanThreads) {
+    if (tgt[r] != ignore_index) {
+      s += loss[r];
+      n += 1.f;
+    }
+  }
+  s = group_reduce<kMeanThreads, 0>(s, red);
+  n = group_reduce<kMeanThreads, 0>(n, red);
+  if (threadIdx.x == 0) out[0] = T::from_f(s / n);
+}
+
+template <typename T>
+static int launch_ce(const void* logits, const int64_t* tgt, float* loss, void* out, int64_t rows,
+                     int64_t vocab, int64_t ignore_index, hipStream_t s) {
+  using S = typename T::S;
+  const S* xp = (const S*)logits;
+  RowPlan plan;
+  const bool vec = vocab % T::kVec == 0 && host_aligned16(logits);
+  bool handled = rows == 0;  // no rows: only the mean kernel runs (0 / 0 = NaN, as torch gives)
+  if (!handled && vec && plan_row(vocab / T::kVec, T::kVec, &plan)) {
+    AK_ROW_SWITCH({
+      const dim3 grid((unsigned)cdiv(rows, RowGeom<L>::kRowsPerBlock));
+      ce_rows<T, L, VPT><<<grid, RowGeom<L>::kThreads, 0, s>>>(xp, tgt, loss, rows, (int)vocab, ignore_index);
+    });
+  }
+  if (!handled) ce_loop<T><<<(unsigned)rows, kLoopThreads, 0, s>>>(xp, tgt, loss, (int)vocab, ignore_index);
+  ce_mean<T><<<1, kMeanThreads, 0, s>>>(loss, tgt, (S*)out, rows, ignore_index);
+  return record_launch();
+}
+
+// =============================================================================================
+// Last-dim reductions (reduce over a contiguous row): sum with fp32 accumulation rounded once
+// (x.sum(-1), reference.py:72-74), max exact with NaN propagation (x.max(-1).values, :76-78).
+// =============================================================================================
+template <typename T, int L, int VPT, bool MAX>
+__global__ __launch_bounds__(RowGeom<L>::kThreads) void reduce_rows(
+    const typename T::S* __restrict__ x, typename T::S* __restrict__ y, int64_t rows, int cols) {
+  using G = RowGeom<L>;
+  using R = RowRegs<T, L, VPT>;
+  __shared__ float red[G::kWPB];
+  const int gl = G::lane_in_row();
+  const int64_t row = (int64_t)blockIdx.x * G::kRowsPerBlock + G::group();
+  const bool active = row < rows;
+  const int nvec = active ? cols / T::kVec : 0;
+  R r;
+  r.load(x + row * cols, nvec, gl);
+  float a = MAX ? -INFINITY : 0.f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j)
+    if (R::valid(j, gl, nvec))
+#pragma unroll
+      for (int e = 0; e < T::kVec; ++e) a = MAX ? nan_max(a, r.f[j * T::kVec + e]) : a + r.f[j * T::kVec + e];
+  a = group_reduce<L, MAX ? 2 : 0>(a, red);
+  if (active && gl == 0) y[row] = T::from_f(a);
+}
+
+template <typename T, bool MAX>
+__global__ __launch_bounds__(kLoopThreads) void reduce_loop(const typename T::S* __restrict__ x,
+                                                            typename T::S* __restrict__ y, int cols) {
+  __shared__ float red[kLoopThreads / kWave];
+  const typename T::S* xr = x + (int64_t)blockIdx.x * cols;
+  float a = MAX ? -INFINITY : 0.f;
+  for (int c = threadIdx.x; c < cols; c += kLoopThreads) {
+    const float v = T::to_f(xr[c]);
+    a = MAX ? nan_max(a, v) : a + v;
+  }
+  a = block_reduce<MAX ? 2 : 0>(a, red);
+  if (threadIdx.x == 0) y[blockIdx.x] = T::from_f(a);
+}
+
+// Reduction over a strided middle dim: x viewed as [outer, reduce, inner], one thread per
+// (outer, inner) output; consecutive threads read consecutive inner elements (coalesced).
+template <typename T, bool MAX>
+__global__ __launch_bounds__(256) void reduce_cols(const typename T::S* __restrict__ x,
+                                                   typename T::S* __restrict__ y, int64_t outer,
+                                                   int64_t red_n, int64_t inner) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= outer * inner) return;
+  const int64_t o = i / inner, c = i % inner;
+  const typename T::S* p = x + o * red_n * inner + c;
+  float a = MAX ? -INFINITY : 0.f;
+  for (int64_t r = 0; r < red_n; ++r) {
+    const float v = T::to_f(p[r * inner]);
+    a = MAX ? nan_max(a, v) : a + v;
+  }
+  y[i] = T::from_f(a);
+}
+
+template <typename T, bool MAX>
+static int launch_reduce(const void* x, void* y, int64_t outer, int64_t red_n, int64_t inner,
+                         hipStream_t s) {
+  using S = typename T::S;
+  const S* xp = (const S*)x;
+  S* yp = (S*)y;
+  if (inner == 1) {
+    const int64_t rows = outer, cols = red_n;
+    RowPlan plan;
+    const bool vec = cols % T::kVec == 0 && host_aligned16(x);
+    bool handled = false;
+    if (vec && plan_row(cols / T::kVec, T::kVec, &plan)) {
+      AK_ROW_SWITCH({
+        const dim3 grid((unsigned)cdiv(rows, RowGeom<L>::kRowsPerBlock));
+        reduce_rows<T, L, VPT, MAX><<<grid, RowGeom<L>::kThreads, 0, s>>>(xp, yp, rows, (int)cols);
+      });
+    }
+    if (!handled) reduce_loop<T, MAX><<<(unsigned)rows, kLoopThreads, 0, s>>>(xp, yp, (int)cols);
+  } else {
+    reduce_cols<T, MAX><<<(unsigned)cdiv(outer * inner, 256), 256, 0, s>>>(xp, yp, outer, red_n, inner);
+  }
+  return record_launch();
+}
+
+}  // namespace ak
+
+using namespace ak;
+
+static bool bad_rows(int64_t rows, int64_t cols) {
+  return rows < 0 || cols < 0 || cols > INT_MAX || rows > (int64_t)INT_MAX;
+}
+
+extern "C" int ak_rmsnorm(int dtype, const void* x, const void* w, void* y, int64_t rows,
+                          int64_t cols, float eps, hipStream_t stream) {
+  if (bad_rows(rows, cols)) return AK_EINVAL;
+  if (rows == 0 || cols == 0) return AK_OK;
+  if (!x || !w || !y) return AK_EINVAL;
+  AK_DISPATCH(dtype, T, return launch_rmsnorm<T>(x, w, y, rows, cols, eps, stream));
+}
+
+extern "C" int ak_layernorm(int dtype, const void* x, const void* w, const void* b, void* y,
+                            int64_t rows, int64_t cols, float eps, hipStream_t stream) {
+  if (bad_rows(rows, cols)) return AK_EINVAL;
+  if (rows == 0 || cols == 0) return AK_OK;
+  if (!x || !y) return AK_EINVAL;
+  AK_DISPATCH(dtype, T, return launch_layernorm<T>(x, w, b, y, rows, cols, eps, stream));
+}
+
+extern "C" int ak_softmax(int dtype, const void* x, void* y, int64_t rows, int64_t cols,
+                          hipStream_t stream) {
+  if (bad_rows(rows, cols)) return AK_EINVAL;
+  if (rows == 0 || cols == 0) return AK_OK;
+  if (!x || !y) return AK_EINVAL;
+  AK_DISPATCH(dtype, T, return launch_softmax<T>(x, y, rows, cols, stream));
+}
+
+extern "C" int ak_cross_entropy(int dtype, const void* logits, const int64_t* targets,
+                                float* row_loss, void* out, int64_t rows, int64_t vocab,
+                                int64_t ignore_index, hipStream_t stream) {
+  if (bad_rows(rows, vocab)) return AK_EINVAL;
+  if (!out) return AK_EINVAL;
+  if (rows > 0 && (!logits || !targets || !row_loss || vocab == 0)) return AK_EINVAL;
+  AK_DISPATCH(dtype, T, return launch_ce<T>(logits, targets, row_loss, out, rows, vocab, ignore_index, stream));
+}
+
+extern "C" int ak_reduce_sum(int dtype, const void* x, void* y, int64_t outer, int64_t reduce,
+                             int64_t inner, hipStream_t stream) {
+  if (outer < 0 || reduce < 0 || inner < 0 || reduce > INT_MAX || outer > (int64_t)INT_MAX * 256) return AK_EINVAL;
+  if (outer == 0 || inner == 0) return AK_OK;
+  if (!x || !y) return AK_EINVAL;
+  AK_DISPATCH(dtype, T, return launch_reduce<T, false>(x, y, outer, reduce, inner, stream));
+}
+
+extern "C" int ak_reduce_max(int dtype, const void* x, void* y, int64_t outer, int64_t reduce,
+                             int64_t inner, hipStream_t stream) {
+  if (outer < 0 || reduce <= 0 || inner < 0 || reduce > INT_MAX || outer > (int64_t)INT_MAX * 256) return AK_EINVAL;
+  if (outer == 0 || inner == 0) return AK_OK;
+  if (!x || !y) return AK_EINVAL;
+  AK_DISPATCH(dtype, T, return launch_reduce<T, true>(x, y, outer, reduce, inner, stream));
+}

@@ -1,0 +1,29 @@
+"""Helpers shared by the kernel_fn modules: device guard and row flattening."""
+from __future__ import annotations
+
+import contextlib
+
+import torch
+
+
+def device_guard(t: torch.Tensor):
+    """Make t's device current for the launch when it is not already."""
+    if t.device.index is not None and t.device.index != torch.cuda.current_device():
+        return torch.cuda.device(t.device)
+    return contextlib.nullcontext()
+
+
+def rows_view(x: torch.Tensor) -> torch.Tensor:
+    """[..., N] -> contiguous [rows, N] (a view when x is already contiguous)."""
+    if x.dim() == 0:
+        x = x.reshape(1, 1)
+    elif x.dim() == 1:
+        x = x.reshape(1, -1)
+    x = x.contiguous()
+    return x.view(-1, x.shape[-1])
+
+
+def match_dtype(t: torch.Tensor | None, dtype: torch.dtype) -> torch.Tensor | None:
+    if t is None or t.dtype == dtype:
+        return t
+    return t.to(dtype)

@@ -1,0 +1,68 @@
+"""Flash-attention drop-in: kernel_fn(Q, K, V, causal=True, sm_scale=None).
+
+Mirrors reference.py:32-42 and kernels/flash_attention.py:130: Q, K, V [batch, heads, seq, D]
+(3-D [heads, seq, D] also accepted), default scale D**-0.5, causal mask j > i (top-left aligned).
+K / V may carry fewer heads than Q when the head count divides (grouped-query attention; one KV
+head broadcasts, as the reference's matmul does). Strided views with a contiguous last dim are
+read in place, so [B, S, H, D] tensors need no transpose copy. f16 / bf16, D in {64, 128}.
+Runs ak_flash_attn_fwd (attention.hip).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ._common import device_guard
+
+KERNEL_TYPE = "flash_attention"
+
+
+def _prep(t: torch.Tensor) -> torch.Tensor:
+    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, causal: bool = True,
+              sm_scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """4-D entry point: Q [B, Hq, Sq, D], K / V [B, Hkv, Sk, D]; out may be a strided view."""
+    B, Hq, Sq, D = Q.shape
+    Bk, Hkv, Sk, Dk = K.shape
+    if V.shape != K.shape or Dk != D or Bk != B:
+        raise ValueError(f"flash_attention: shapes Q{tuple(Q.shape)} K{tuple(K.shape)} V{tuple(V.shape)}")
+    if Hkv == 0 or Hq % Hkv:
+        raise ValueError(f"flash_attention: {Hq} query heads not a multiple of {Hkv} KV heads")
+    if not (Q.dtype == K.dtype == V.dtype):
+        raise ValueError("flash_attention: Q, K, V dtypes differ")
+    if Q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"flash_attention: dtype {Q.dtype} unsupported (float16, bfloat16)")
+    if D not in (64, 128):
+        raise ValueError(f"flash_attention: head_dim {D} unsupported (64, 128)")
+    code = _lib.dtype_code(Q, "flash_attention")
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    Q, K, V = _prep(Q), _prep(K), _prep(V)
+    O = out if out is not None else torch.empty((B, Hq, Sq, D), device=Q.device, dtype=Q.dtype)
+    if Sk == 0:
+        raise ValueError("flash_attention: empty key sequence")
+    a = [_lib.i64_array(t.stride()[:3]) for t in (Q, K, V, O)]
+    with device_guard(Q):
+        st = _lib.load().ak_flash_attn_fwd(code, Q.data_ptr(), K.data_ptr(), V.data_ptr(),
+                                           O.data_ptr(), B, Hq, Hkv, Sq, Sk, D, a[0], a[1], a[2],
+                                           a[3], int(bool(causal)), float(sm_scale),
+                                           _lib.stream_of(Q))
+    _lib.check(st, "ak_flash_attn_fwd", Q=tuple(Q.shape), K=tuple(K.shape), dtype=Q.dtype)
+    return O
+
+
+def kernel_fn(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, causal: bool = True,
+              sm_scale: float | None = None) -> torch.Tensor:
+    _lib.require_gpu("flash_attention", Q, K, V)
+    if Q.dim() == 3:
+        return attention(Q[None], K[None], V[None], causal, sm_scale)[0]
+    if Q.dim() != 4:
+        raise ValueError(f"flash_attention: expected 3-D or 4-D Q, got {Q.dim()}-D")
+    if K.shape[0] != Q.shape[0] and K.shape[0] == 1:
+        K = K.expand(Q.shape[0], *K.shape[1:])
+        V = V.expand(Q.shape[0], *V.shape[1:])
+    return attention(Q, K, V, causal, sm_scale)

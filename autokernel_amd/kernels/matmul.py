@@ -1,0 +1,72 @@
+"""Matmul drop-in: kernel_fn(A, B) = torch.matmul(A, B).
+
+Mirrors reference.py:10-12 and kernels/matmul.py:62. A: [..., M, K] (leading dims flattened into
+M when B is 2-D), B: [K, N]; batched B loops over the batch. When B is a transposed view of a
+row-major [N, K] tensor (nn.Linear's weight.t()), the GEMM reads it in place (b_trans = 1)
+instead of copying. Runs ak_gemm (gemm.hip).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ._common import device_guard
+
+KERNEL_TYPE = "matmul"
+
+
+def _b_layout(B: torch.Tensor) -> tuple[torch.Tensor, int, int]:
+    """(tensor, ldb, b_trans) for a 2-D B [K, N] without copying when possible."""
+    K, N = B.shape
+    if B.stride(1) == 1 and B.stride(0) >= max(N, 1):
+        return B, B.stride(0), 0
+    if B.stride(0) == 1 and B.stride(1) >= max(K, 1):
+        return B, B.stride(1), 1
+    Bc = B.contiguous()
+    return Bc, max(N, 1), 0
+
+
+def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = A @ B for 2-D A [M, K] and 2-D B [K, N] (B may be a transposed [N, K] view)."""
+    M, K = A.shape
+    K2, N = B.shape
+    if K != K2:
+        raise ValueError(f"matmul: shapes {tuple(A.shape)} and {tuple(B.shape)} do not align")
+    if A.dtype != B.dtype:
+        raise ValueError(f"matmul: dtype mismatch {A.dtype} vs {B.dtype}")
+    code = _lib.dtype_code(A, "matmul")
+    if not (A.stride(1) == 1 and A.stride(0) >= max(K, 1)):
+        A = A.contiguous()
+    lda = A.stride(0) if M > 1 else max(K, 1)
+    Bt, ldb, bt = _b_layout(B)
+    C = out if out is not None else torch.empty((M, N), device=A.device, dtype=A.dtype)
+    if K == 0:
+        return C.zero_()
+    with device_guard(A):
+        st = _lib.load().ak_gemm(code, A.data_ptr(), Bt.data_ptr(), C.data_ptr(), M, N, K,
+                                 lda, ldb, C.stride(0) if M > 1 else max(N, 1), bt,
+                                 _lib.stream_of(A))
+    _lib.check(st, "ak_gemm", M=M, N=N, K=K, b_trans=bt, dtype=A.dtype)
+    return C
+
+
+def kernel_fn(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    _lib.require_gpu("matmul", A, B)
+    if A.dim() == 1 and B.dim() == 1:
+        return gemm(A.view(1, -1), B.view(-1, 1)).view(())
+    if A.dim() == 1:
+        return kernel_fn(A.view(1, -1), B).squeeze(-2)
+    if B.dim() == 1:
+        return kernel_fn(A, B.view(-1, 1)).squeeze(-1)
+    if B.dim() == 2:
+        lead = A.shape[:-1]
+        A2 = A.reshape(-1, A.shape[-1]) if A.dim() > 2 else A
+        return gemm(A2, B).view(*lead, B.shape[-1])
+    # batched B: broadcast batch dims, one GEMM per batch entry
+    batch = torch.broadcast_shapes(A.shape[:-2], B.shape[:-2])
+    Ab = A.expand(*batch, *A.shape[-2:]).reshape(-1, *A.shape[-2:])
+    Bb = B.expand(*batch, *B.shape[-2:]).reshape(-1, *B.shape[-2:])
+    C = torch.empty((Ab.shape[0], A.shape[-2], B.shape[-1]), device=A.device, dtype=A.dtype)
+    for i in range(Ab.shape[0]):
+        gemm(Ab[i], Bb[i], out=C[i])
+    return C.view(*batch, A.shape[-2], B.shape[-1])

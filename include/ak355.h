@@ -1,0 +1,153 @@
+/*
+ * ak355.h -- C ABI of libak355.so, the MI355X (gfx950) kernels behind AutoKernel's nine-op suite.
+ *
+ * Every entry point:
+ *   - takes device pointers, element counts and scalars only (no framework types);
+ *   - launches asynchronously on the caller's HIP stream `stream` (pass torch's current stream);
+ *   - never allocates, frees or synchronises; every buffer (outputs, workspaces) is the caller's;
+ *   - keeps no mutable global state, so concurrent calls on different streams are safe;
+ *   - returns AK_OK or an ak_status code; AK_EHIP means a HIP launch error
+ *     (its text is available from ak_last_hip_error_string() on the calling thread).
+ *
+ * Tensors are dense and row-major unless a leading-dimension / stride argument says otherwise.
+ * Element types are given by an ak_dtype code; f16 and bf16 are IEEE binary16 and bfloat16.
+ *
+ * The "replaces" notes name the reference interface each entry point stands in for
+ * (paths relative to RightNow-AI/autokernel).
+ */
+#ifndef AK355_H
+#define AK355_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum ak_dtype {
+    AK_F32 = 0,
+    AK_F16 = 1,
+    AK_BF16 = 2
+} ak_dtype;
+
+typedef enum ak_status {
+    AK_OK = 0,
+    AK_EINVAL = 1,        /* bad argument: null pointer, negative size, bad dtype */
+    AK_EUNSUPPORTED = 2,  /* valid request this build has no kernel for (e.g. head_dim 96) */
+    AK_EHIP = 3           /* kernel launch failed; see ak_last_hip_error_string() */
+} ak_status;
+
+typedef enum ak_activation {
+    AK_ACT_SILU = 0,   /* x * sigmoid(x)                 (reference.py:49-50) */
+    AK_ACT_GELU = 1,   /* exact erf GELU, F.gelu default (reference.py:51-52) */
+    AK_ACT_RELU2 = 2,  /* relu(x)^2                      (reference.py:53-54) */
+    AK_ACT_NONE = 3    /* identity: gate passed through  (reference.py: unknown activation string) */
+} ak_activation;
+
+/* Library identity and diagnostics. */
+const char* ak_version(void);
+const char* ak_status_string(int status);
+const char* ak_last_hip_error_string(void);
+
+/*
+ * RMSNorm over the last dim: y = (x / sqrt(mean(x*x) + eps)) * w, each step rounded to the
+ * element type as the reference's tensor op sequence does.
+ * x, y: [rows, cols]; w: [cols].
+ * Replaces: reference.py:26-29 rmsnorm_ref; kernels/cuda/rmsnorm.py:132-158 rmsnorm_cuda;
+ *           kernels/rmsnorm.py:45 kernel_fn(x, weight, eps).
+ */
+int ak_rmsnorm(int dtype, const void* x, const void* w, void* y,
+               int64_t rows, int64_t cols, float eps, hipStream_t stream);
+
+/*
+ * LayerNorm over the last dim with fp32 statistics: y = (x - mean) * rsqrt(var + eps) * w + b.
+ * w or b may be NULL (treated as ones / zeros). x, y: [rows, cols]; w, b: [cols].
+ * Replaces: reference.py:20-23 layernorm_ref; kernels/cuda/layernorm.py:268-307 layernorm_cuda.
+ */
+int ak_layernorm(int dtype, const void* x, const void* w, const void* b, void* y,
+                 int64_t rows, int64_t cols, float eps, hipStream_t stream);
+
+/*
+ * Softmax over the last dim with fp32 internals, one output rounding. x, y: [rows, cols].
+ * Replaces: reference.py:15-17 softmax_ref; kernels/cuda/softmax.py:187-232 softmax_cuda.
+ */
+int ak_softmax(int dtype, const void* x, void* y, int64_t rows, int64_t cols, hipStream_t stream);
+
+/*
+ * Interleaved rotary embedding. x, y: [rows, head_dim]; cos, sin: [table_rows, head_dim/2].
+ * Row r of x uses table row (r / rep_inner) % table_rows, which covers the [.., S, D] layout
+ * (rep_inner = 1) and the [B, S, H, D] layout (rep_inner = H).
+ *   y[2i]   = x[2i]*cos[i] - x[2i+1]*sin[i]
+ *   y[2i+1] = x[2i]*sin[i] + x[2i+1]*cos[i]   (every product and sum rounded to the element type)
+ * Replaces: reference.py:63-69 rotary_embedding_ref; kernels/cuda/rotary_embedding.py:100-125.
+ */
+int ak_rope(int dtype, const void* x, const void* cos_t, const void* sin_t, void* y,
+            int64_t rows, int64_t head_dim, int64_t table_rows, int64_t rep_inner,
+            hipStream_t stream);
+
+/*
+ * Mean cross-entropy over rows: out = mean_r( logsumexp(x_r) - x_r[t_r] ), rows whose target is
+ * ignore_index excluded from sum and count (F.cross_entropy semantics). A target outside
+ * [0, vocab) that is not ignore_index makes the result NaN.
+ * logits: [rows, vocab]; targets: int64 [rows]; row_loss: fp32 workspace [rows] (caller-owned);
+ * out: one element of the logits' dtype.
+ * Replaces: reference.py:58-60 cross_entropy_ref; kernels/cuda/cross_entropy.py:116-138.
+ */
+int ak_cross_entropy(int dtype, const void* logits, const int64_t* targets, float* row_loss,
+                     void* out, int64_t rows, int64_t vocab, int64_t ignore_index,
+                     hipStream_t stream);
+
+/*
+ * Sum / max over the middle dim of x viewed as [outer, reduce, inner]; y: [outer, inner].
+ * Sum accumulates in fp32 with a fixed order (deterministic); max propagates NaN like torch.max.
+ * Replaces: reference.py:72-78 reduce_sum_ref / reduce_max_ref; kernels/cuda/reduce.py:79-98;
+ *           kernels/reduce.py:51-140 kernel_fn(x, dim).
+ */
+int ak_reduce_sum(int dtype, const void* x, void* y, int64_t outer, int64_t reduce,
+                  int64_t inner, hipStream_t stream);
+int ak_reduce_max(int dtype, const void* x, void* y, int64_t outer, int64_t reduce,
+                  int64_t inner, hipStream_t stream);
+
+/*
+ * GEMM with fp32 accumulation and one output rounding: C[M,N] = A[M,K] * op(B).
+ *   b_trans = 0: B is [K, N] with row stride ldb  (torch.matmul(A, B), reference.py:10-12)
+ *   b_trans = 1: B is [N, K] with row stride ldb  (x @ W.T for an nn.Linear weight W)
+ * lda / ldc are the row strides of A and C in elements.
+ * Replaces: reference.py:10-12 matmul_ref; kernels/cuda/matmul.py:210-233 matmul_cuda;
+ *           verify.py:429-430 (the Linear path, without its per-call weight transpose copy).
+ */
+int ak_gemm(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+            int64_t lda, int64_t ldb, int64_t ldc, int b_trans, hipStream_t stream);
+
+/*
+ * Fused gate/up projection of the SwiGLU MLP:
+ *   h = round(act(round(x @ w_gate.T))) * round(x @ w_up.T), rounded to the element type.
+ * x: [M, D]; w_gate, w_up: [H, D] (nn.Linear layout); h: [M, H].
+ * The down projection is ak_gemm(h, w_down, b_trans = 1).
+ * Replaces: reference.py:45-55 fused_mlp_ref (gate/up/activation/product);
+ *           kernels/cuda/fused_mlp.py:115-157 fused_mlp_cuda.
+ */
+int ak_mlp_gate_up(int dtype, const void* x, const void* w_gate, const void* w_up, void* h,
+                   int64_t M, int64_t H, int64_t D, int activation, hipStream_t stream);
+
+/*
+ * Flash-attention forward: O = softmax(Q K^T * sm_scale [+ causal mask]) V per (batch, head).
+ * Q, O: [B, Hq, Sq, D]-indexed, K, V: [B, Hkv, Sk, D]-indexed, each given by element strides
+ * (batch, head, seq); the last dim is contiguous. Hq must be a multiple of Hkv (grouped-query
+ * attention: query head h reads KV head h / (Hq / Hkv)). causal masks key j > query i
+ * (top-left aligned, as torch.triu(ones(Sq, Sk), 1) does). D in {64, 128}. f16 / bf16.
+ * Replaces: reference.py:32-42 flash_attention_ref; kernels/cuda/flash_attention.py:207-235;
+ *           kernels/flash_attention.py:130 kernel_fn(Q, K, V, causal, sm_scale).
+ */
+int ak_flash_attn_fwd(int dtype, const void* Q, const void* K, const void* V, void* O,
+                      int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                      const int64_t* q_strides, const int64_t* k_strides,
+                      const int64_t* v_strides, const int64_t* o_strides,
+                      int causal, float sm_scale, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AK355_H */

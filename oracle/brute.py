@@ -1,0 +1,145 @@
+"""Independent numpy restatements that pin oracle.reference_ops (test infrastructure only).
+
+Two kinds:
+  * float64 brute force of the mathematics (any input dtype, compared with a tolerance);
+  * float16 / float32 step-by-step emulations of the reference's op sequence for the ops whose
+    per-op rounding is the point (rmsnorm: x**2 rounds and may overflow before the mean;
+    rotary embedding: every product and sum rounds). numpy's float16 arithmetic rounds each
+    operation to binary16 exactly like a torch f16 tensor op, so these are bit-comparable.
+No torch import: these share no code with the thing they check.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+try:
+    from scipy.special import erf as _erf
+except Exception:  # pragma: no cover - scipy is present in this image
+    _erf = np.vectorize(math.erf)
+
+
+def f64(a) -> np.ndarray:
+    return np.asarray(a, dtype=np.float64)
+
+
+# ------------------------------------------------------------------------------------- float64
+def matmul(A, B):
+    return f64(A) @ f64(B)
+
+
+def softmax(x, axis=-1):
+    x = f64(x)
+    m = np.max(x, axis=axis, keepdims=True)
+    e = np.exp(x - m)
+    return e / np.sum(e, axis=axis, keepdims=True)
+
+
+def layernorm(x, w, b, eps=1e-5):
+    x = f64(x)
+    mu = x.mean(-1, keepdims=True)
+    var = ((x - mu) ** 2).mean(-1, keepdims=True)
+    y = (x - mu) / np.sqrt(var + eps)
+    if w is not None:
+        y = y * f64(w)
+    if b is not None:
+        y = y + f64(b)
+    return y
+
+
+def rmsnorm(x, w, eps=1e-6):
+    x = f64(x)
+    return x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * f64(w)
+
+
+def rope(x, cos, sin):
+    x = f64(x)
+    e, o = x[..., 0::2], x[..., 1::2]
+    c, s = f64(cos), f64(sin)
+    out = np.empty(np.broadcast_shapes(e.shape, c.shape)[:-1] + (x.shape[-1],))
+    out[..., 0::2] = e * c - o * s
+    out[..., 1::2] = e * s + o * c
+    return out
+
+
+def cross_entropy(logits, targets, ignore_index=-100):
+    x = f64(logits).reshape(-1, np.shape(logits)[-1])
+    t = np.asarray(targets).reshape(-1)
+    m = x.max(-1)
+    lse = m + np.log(np.exp(x - m[:, None]).sum(-1))
+    keep = t != ignore_index
+    rows = np.nonzero(keep)[0]
+    if rows.size == 0:
+        return float("nan")
+    return float(np.mean(lse[rows] - x[rows, t[rows]]))
+
+
+def reduce_sum(x, axis=-1):
+    return f64(x).sum(axis)
+
+
+def reduce_max(x, axis=-1):
+    return np.max(np.asarray(x), axis=axis)
+
+
+def attention(Q, K, V, causal=True, sm_scale=None):
+    Q, K, V = f64(Q), f64(K), f64(V)
+    if sm_scale is None:
+        sm_scale = Q.shape[-1] ** -0.5
+    s = (Q @ np.swapaxes(K, -1, -2)) * sm_scale
+    if causal:
+        sq, sk = Q.shape[-2], K.shape[-2]
+        s = np.where(np.triu(np.ones((sq, sk), dtype=bool), 1), -np.inf, s)
+    return softmax(s) @ V
+
+
+def gelu_erf(x):
+    x = f64(x)
+    return 0.5 * x * (1.0 + _erf(x / math.sqrt(2.0)))
+
+
+def fused_mlp(x, wg, wu, wd, activation="silu"):
+    x = f64(x)
+    g = x @ f64(wg).T
+    u = x @ f64(wu).T
+    if activation == "silu":
+        g = g / (1.0 + np.exp(-g))
+    elif activation == "gelu":
+        g = gelu_erf(g)
+    elif activation == "relu2":
+        g = np.maximum(g, 0.0) ** 2
+    return (g * u) @ f64(wd).T
+
+
+# ----------------------------------------------------------- step-by-step rounding emulations
+def rmsnorm_steps(x, w, eps=1e-6):
+    """reference.py:28-29 step by step in x's numpy dtype (float16 or float32).
+
+    x**2 rounds (float16 overflows to inf past 255.9), the mean accumulates the rounded squares in
+    float64 and rounds once, then + eps, sqrt, divide and multiply each round.
+    """
+    x = np.asarray(x)
+    dt = x.dtype.type
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        sq = (x * x).astype(dt)
+        ms = dt(1) * (sq.astype(np.float64).sum(-1, keepdims=True) / x.shape[-1]).astype(dt)
+        t = (ms.astype(np.float32) + np.float32(eps)).astype(dt)
+        rms = np.sqrt(t.astype(np.float32)).astype(dt)
+        q = (x.astype(np.float32) / rms.astype(np.float32)).astype(dt)
+        return (q.astype(np.float32) * np.asarray(w).astype(np.float32)).astype(dt)
+
+
+def rope_steps(x, cos, sin):
+    """reference.py:65-69 step by step in the numpy dtype of x (float16 / float32): bit-exact."""
+    x = np.asarray(x)
+    dt = x.dtype.type
+    c, s = np.asarray(cos).astype(dt), np.asarray(sin).astype(dt)
+    e, o = x[..., 0::2], x[..., 1::2]
+    with np.errstate(over="ignore", invalid="ignore"):
+        a = (e * c).astype(dt) - (o * s).astype(dt)
+        b = (e * s).astype(dt) + (o * c).astype(dt)
+    out = np.empty(a.shape[:-1] + (x.shape[-1],), dtype=dt)
+    out[..., 0::2] = a.astype(dt)
+    out[..., 1::2] = b.astype(dt)
+    return out

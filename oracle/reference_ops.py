@@ -1,0 +1,108 @@
+"""PyTorch-CPU restatement of the reference's reference.py (test infrastructure only).
+
+Each function follows the reference function cited beside it op for op: every intermediate is a
+tensor of the input's dtype, so the rounding points (and f16 overflow to inf) are the
+reference's. Inputs are moved to the CPU; results come back on the CPU.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+
+def _cpu(*ts):
+    return [t.detach().cpu() if isinstance(t, torch.Tensor) else t for t in ts]
+
+
+def matmul_ref(A, B):
+    """reference.py:10-12 -- torch.matmul(A, B)."""
+    A, B = _cpu(A, B)
+    return torch.matmul(A, B)
+
+
+def softmax_ref(x, dim=-1):
+    """reference.py:15-17 -- F.softmax(x, dim)."""
+    (x,) = _cpu(x)
+    return F.softmax(x, dim=dim)
+
+
+def layernorm_ref(x, weight, bias, eps=1e-5):
+    """reference.py:20-23 -- F.layer_norm over the last dim."""
+    x, weight, bias = _cpu(x, weight, bias)
+    return F.layer_norm(x, x.shape[-1:], weight, bias, eps)
+
+
+def rmsnorm_ref(x, weight, eps=1e-6):
+    """reference.py:26-29 -- rms = sqrt(mean(x**2, -1) + eps); (x / rms) * weight."""
+    x, weight = _cpu(x, weight)
+    sq = x ** 2
+    rms = torch.sqrt(torch.mean(sq, dim=-1, keepdim=True) + eps)
+    return (x / rms) * weight
+
+
+def flash_attention_ref(Q, K, V, causal=True, sm_scale=None):
+    """reference.py:32-42 -- (Q K^T) * scale, triu(…, 1) mask to -inf, softmax, @ V."""
+    Q, K, V = _cpu(Q, K, V)
+    if sm_scale is None:
+        sm_scale = Q.shape[-1] ** -0.5
+    scores = torch.matmul(Q, K.transpose(-2, -1)) * sm_scale
+    if causal:
+        sq, sk = Q.shape[-2], K.shape[-2]
+        upper = torch.triu(torch.ones(sq, sk, dtype=torch.bool), diagonal=1)
+        scores = scores.masked_fill(upper, float("-inf"))
+    return torch.matmul(F.softmax(scores, dim=-1), V)
+
+
+def fused_mlp_ref(x, w_gate, w_up, w_down, activation="silu"):
+    """reference.py:45-55 -- act(x @ w_gate.T) * (x @ w_up.T) @ w_down.T, each step materialised."""
+    x, w_gate, w_up, w_down = _cpu(x, w_gate, w_up, w_down)
+    g = x @ w_gate.T
+    u = x @ w_up.T
+    if activation == "silu":
+        g = F.silu(g)
+    elif activation == "gelu":
+        g = F.gelu(g)
+    elif activation == "relu2":
+        g = F.relu(g) ** 2
+    return (g * u) @ w_down.T
+
+
+def cross_entropy_ref(logits, targets):
+    """reference.py:58-60 -- F.cross_entropy(logits.view(-1, V), targets.view(-1))."""
+    logits, targets = _cpu(logits, targets)
+    return F.cross_entropy(logits.view(-1, logits.size(-1)), targets.view(-1))
+
+
+def rotary_embedding_ref(x, cos, sin):
+    """reference.py:63-69 -- interleaved pairs rotated, each product / sum rounded."""
+    x, cos, sin = _cpu(x, cos, sin)
+    even, odd = x[..., 0::2], x[..., 1::2]
+    out_even = even * cos - odd * sin
+    out_odd = even * sin + odd * cos
+    return torch.stack((out_even, out_odd), dim=-1).flatten(-2)
+
+
+def reduce_sum_ref(x, dim=-1):
+    """reference.py:72-74 -- x.sum(dim)."""
+    (x,) = _cpu(x)
+    return x.sum(dim=dim)
+
+
+def reduce_max_ref(x, dim=-1):
+    """reference.py:76-78 -- x.max(dim).values."""
+    (x,) = _cpu(x)
+    return x.max(dim=dim).values
+
+
+REFERENCE = {
+    "matmul": lambda i: matmul_ref(i["A"], i["B"]),
+    "softmax": lambda i: softmax_ref(i["x"]),
+    "layernorm": lambda i: layernorm_ref(i["x"], i["weight"], i["bias"]),
+    "rmsnorm": lambda i: rmsnorm_ref(i["x"], i["weight"]),
+    "flash_attention": lambda i: flash_attention_ref(i["Q"], i["K"], i["V"]),
+    "fused_mlp": lambda i: fused_mlp_ref(i["x"], i["w_gate"], i["w_up"], i["w_down"]),
+    "cross_entropy": lambda i: cross_entropy_ref(i["logits"], i["targets"]),
+    "rotary_embedding": lambda i: rotary_embedding_ref(i["x"], i["cos"], i["sin"]),
+    "reduce": lambda i: reduce_sum_ref(i["x"]),
+}
+"""Keyword-dict wrappers in the style of the reference harness's _ref_* (bench.py:284-318)."""
