@@ -358,6 +358,13 @@ __global__ __launch_bounds__(256) void gemm_f32(const float* __restrict__ A, con
   for (int kt = 0; kt < KT; ++kt) {
     const int cur = kt & 1;
     if (kt + 1 < KT) gload((kt + 1) * BK);
+    // Two-level sum: each k-tile accumulates from zero and is then added to the total, which
+    // keeps fp32 rounding error of long dot products about sqrt(BK) times smaller.
+    f32x4 part[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) part[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < BK / 4; ++s) {
       const int k = s * 4 + fk;
@@ -372,8 +379,12 @@ __global__ __launch_bounds__(256) void gemm_f32(const float* __restrict__ A, con
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fb[j], fa[i], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 4; ++j) part[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fb[j], fa[i], part[i][j], 0, 0, 0);
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] += part[i][j];
     if (kt + 1 < KT) sstore(cur ^ 1);
     __syncthreads();
   }
@@ -518,6 +529,11 @@ __global__ __launch_bounds__(256) void gate_up_f32(const float* __restrict__ X, 
       sU[row * PA + k] = (n0 + row < H && kin) ? Wu[(int64_t)(n0 + row) * D + k0 + k] : 0.f;
     }
     __syncthreads();
+    f32x4 pg[2][2], pu[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) pg[i][j] = pu[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < BK / 4; ++s) {
       const int k = s * 4 + fk;
@@ -533,10 +549,17 @@ __global__ __launch_bounds__(256) void gate_up_f32(const float* __restrict__ X, 
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          ag[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fg[j], fx[i], ag[i][j], 0, 0, 0);
-          au[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fu[j], fx[i], au[i][j], 0, 0, 0);
+          pg[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fg[j], fx[i], pg[i][j], 0, 0, 0);
+          pu[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fu[j], fx[i], pu[i][j], 0, 0, 0);
         }
     }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        ag[i][j] += pg[i][j];
+        au[i][j] += pu[i][j];
+      }
     __syncthreads();
   }
 #pragma unroll

@@ -83,6 +83,34 @@ __global__ __launch_bounds__(256) void rope_scalar(const typename T::S* __restri
   y[2 * i] = T::from_f(y1);
   y[2 * i + 1] = T::from_f(y2);
 }
+// Model form (the reference's LLaMA apply_rotary_emb, models/llama_7b.py:40-48): x upcast to
+// fp32, rotated by fp32 cos / sin as a complex multiply, rounded once to x's dtype.
+template <typename T>
+__global__ __launch_bounds__(256) void rope_f32t_vec(const typename T::S* __restrict__ x,
+                                                    const float* __restrict__ ct,
+                                                    const float* __restrict__ st,
+                                                    typename T::S* __restrict__ y, int64_t nchunks,
+                                                    int chunks_per_row, int half, int64_t table_rows,
+                                                    int64_t rep_inner) {
+  constexpr int kP = T::kVec / 2;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nchunks) return;
+  const int64_t row = i / chunks_per_row;
+  const int c = (int)(i - row * chunks_per_row);
+  const int64_t trow = (row / rep_inner) % table_rows;
+  const u32x4 xv = ld16(x + i * T::kVec);
+  const float* cp = ct + trow * half + c * kP;
+  const float* sp = st + trow * half + c * kP;
+  u32x4 yv;
+#pragma unroll
+  for (int p = 0; p < kP; ++p) {
+    const float a = T::lane_elem(xv, 2 * p), b = T::lane_elem(xv, 2 * p + 1);
+    const float cc = cp[p], ss = sp[p];
+    T::set_elem(yv, 2 * p, a * cc - b * ss);
+    T::set_elem(yv, 2 * p + 1, a * ss + b * cc);
+  }
+  st16(y + i * T::kVec, yv);
+}
 #pragma clang fp contract(on)
 
 template <typename T>
@@ -105,6 +133,17 @@ static int launch_rope(const void* x, const void* c, const void* s, void* y, int
   return record_launch();
 }
 
+template <typename T>
+static int launch_rope_f32t(const void* x, const float* c, const float* s, void* y, int64_t rows,
+                            int64_t d, int64_t table_rows, int64_t rep_inner, hipStream_t stream) {
+  using S = typename T::S;
+  const int cpr = (int)(d / T::kVec);
+  const int64_t n = rows * cpr;
+  rope_f32t_vec<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>((const S*)x, c, s, (S*)y, n, cpr,
+                                                                 (int)(d / 2), table_rows, rep_inner);
+  return record_launch();
+}
+
 }  // namespace ak
 
 using namespace ak;
@@ -117,4 +156,17 @@ extern "C" int ak_rope(int dtype, const void* x, const void* cos_t, const void* 
   if (!x || !cos_t || !sin_t || !y || table_rows <= 0 || rep_inner <= 0) return AK_EINVAL;
   if (rows * head_dim / 2 > (int64_t)UINT_MAX * 256) return AK_EINVAL;
   AK_DISPATCH(dtype, T, return launch_rope<T>(x, cos_t, sin_t, y, rows, head_dim, table_rows, rep_inner, stream));
+}
+
+extern "C" int ak_rope_f32_tables(int dtype, const void* x, const float* cos_t, const float* sin_t,
+                                  void* y, int64_t rows, int64_t head_dim, int64_t table_rows,
+                                  int64_t rep_inner, hipStream_t stream) {
+  if (rows < 0 || head_dim < 0 || head_dim % 2 != 0 || head_dim > INT_MAX) return AK_EINVAL;
+  if (rows == 0 || head_dim == 0) return AK_OK;
+  if (!x || !cos_t || !sin_t || !y || table_rows <= 0 || rep_inner <= 0) return AK_EINVAL;
+  if (dtype != AK_F16 && dtype != AK_BF16) return AK_EUNSUPPORTED;
+  if (head_dim % 8 != 0 || !host_aligned16(x) || !host_aligned16(y)) return AK_EUNSUPPORTED;
+  if (rows * head_dim / 8 > (int64_t)UINT_MAX * 256) return AK_EINVAL;
+  if (dtype == AK_F16) return launch_rope_f32t<TF16>(x, cos_t, sin_t, y, rows, head_dim, table_rows, rep_inner, stream);
+  return launch_rope_f32t<TBF16>(x, cos_t, sin_t, y, rows, head_dim, table_rows, rep_inner, stream);
 }

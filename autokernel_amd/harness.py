@@ -1,0 +1,543 @@
+"""Per-op correctness and roofline harness: the role of the reference's bench.py.
+
+    python -m autokernel_amd.harness --kernel softmax [--quick] [--sizes large] [--profile]
+    python -m autokernel_amd.harness            # the drop-in slot: kernel.py's KERNEL_TYPE / kernel_fn
+
+What it keeps from the reference harness (bench.py):
+  * the five correctness stages and their verdict rules (bench.py:641-966): smoke (abort on
+    failure), shape sweep (OOM = SKIP), numerical stability with the five adversarial transforms
+    and 10x relaxed tolerance (NaN/Inf only allowed where the reference has them), bitwise
+    determinism over three runs, edge sizes;
+  * timing like triton's do_bench (bench.py:973-1000): a cache-clearing write before every timed
+    call, warm-up and repeat budgets in milliseconds, mean reported (median too);
+  * the roofline classification with ridge = peak fp16 / peak bandwidth (bench.py:1065-1082)
+    and the greppable `key: value` output (bench.py:1293-1409).
+What differs: inputs are generated on the CPU and copied (bit-identical inputs everywhere), the
+clearing buffer is 512 MiB (MI355X's Infinity Cache is 256 MB), the MI355X peaks are AMD's
+dense figures (the reference table's 2300 TFLOPS is printed beside them), and the comparison
+baseline is stock PyTorch (baseline_torch), since the product never runs the CPU oracle.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import math
+import os
+import signal
+import sys
+import time
+import traceback
+from dataclasses import dataclass
+from typing import Any, Callable, Dict, Optional
+
+import torch
+
+from . import baseline_torch, spec
+
+
+class BenchTimeoutError(Exception):
+    pass
+
+
+class Timeout:
+    """Wall-clock limit around one kernel_fn call (SIGALRM; main thread only)."""
+
+    def __init__(self, seconds: int):
+        self.seconds = seconds
+        self._armed = False
+
+    def _handler(self, signum, frame):
+        raise BenchTimeoutError(f"timed out after {self.seconds}s")
+
+    def __enter__(self):
+        if hasattr(signal, "SIGALRM") and self.seconds > 0:
+            try:
+                self._old = signal.signal(signal.SIGALRM, self._handler)
+                signal.alarm(self.seconds)
+                self._armed = True
+            except ValueError:  # not the main thread
+                self._armed = False
+        return self
+
+    def __exit__(self, *exc):
+        if self._armed:
+            signal.alarm(0)
+            signal.signal(signal.SIGALRM, self._old)
+        return False
+
+
+# ------------------------------------------------------------------------------- GPU facts
+@dataclass
+class GPUSpec:
+    name: str = "Unknown"
+    cu_count: int = 0
+    memory_gb: float = 0.0
+    peak_tflops_fp16: float = 0.0      # dense MFMA, f16 / bf16
+    peak_tflops_fp32: float = 0.0      # dense MFMA, fp32
+    peak_bandwidth_gb_s: float = 0.0
+    llc_mb: float = 0.0
+    ref_table_tflops_fp16: float = 0.0  # the reference harness's table entry (bench.py:121)
+
+
+MI355X = dict(name="AMD Instinct MI355X", peak_tflops_fp16=2516.6, peak_tflops_fp32=157.3,
+              peak_bandwidth_gb_s=8000.0, llc_mb=256.0, ref_table_tflops_fp16=2300.0)
+
+
+def detect_gpu() -> GPUSpec:
+    if not torch.cuda.is_available():
+        return GPUSpec()
+    p = torch.cuda.get_device_properties(0)
+    arch = getattr(p, "gcnArchName", "") or ""
+    g = GPUSpec(name=p.name or arch, cu_count=p.multi_processor_count,
+                memory_gb=round(p.total_memory / 2 ** 30, 1))
+    if arch.startswith("gfx950"):
+        for k, v in MI355X.items():
+            setattr(g, k, v)
+    return g
+
+
+# ----------------------------------------------------------------------------- comparison
+def compare(output: torch.Tensor, expected: torch.Tensor, atol: float, rtol: float) -> dict:
+    """bench.py:604-633: fp32 cast, shape check, allclose, max / mean error, % within tol."""
+    if output.shape != expected.shape:
+        return {"match": False, "reason": f"shape mismatch: {tuple(output.shape)} vs {tuple(expected.shape)}",
+                "max_abs_error": float("inf"), "mean_abs_error": float("inf"), "pct_within_tol": 0.0}
+    o, e = output.float(), expected.float()
+    d = (o - e).abs()
+    max_abs = d.max().item() if d.numel() else 0.0
+    mean_abs = d.mean().item() if d.numel() else 0.0
+    within = (d <= atol + rtol * e.abs()).float().mean().item() * 100.0 if d.numel() else 100.0
+    match = bool(torch.allclose(o, e, atol=atol, rtol=rtol))
+    return {"match": match, "reason": "" if match else f"max_abs_error={max_abs:.6e} exceeds tol(atol={atol}, rtol={rtol})",
+            "max_abs_error": max_abs, "mean_abs_error": mean_abs, "pct_within_tol": within}
+
+
+def has_nan_inf(t: torch.Tensor) -> bool:
+    return bool(torch.isnan(t).any().item() or torch.isinf(t).any().item())
+
+
+def _is_oom(e: BaseException) -> bool:
+    return isinstance(e, torch.cuda.OutOfMemoryError) or "out of memory" in str(e).lower()
+
+
+def _empty_cache(device: str) -> None:
+    if device.startswith("cuda") and torch.cuda.is_available():
+        torch.cuda.empty_cache()
+
+
+# --------------------------------------------------------------------------- correctness
+def run_correctness(kernel_fn: Callable, config: dict, quick: bool = False, device: str = "cuda",
+                    ref_fn: Optional[Callable] = None, timeout_s: int = 30, log=print) -> dict:
+    """The five stages of bench.py:641-966 with the same verdict rules."""
+    ref_fn = ref_fn or config["reference_fn"]
+    gen = config["input_generator"]
+    sizes, dtypes, tols = config["test_sizes"], config["test_dtypes"], config["tolerances"]
+    res: Dict[str, Any] = {"smoke_test": "SKIP", "shape_sweep": "SKIP", "numerical_stability": "SKIP",
+                           "determinism": "SKIP", "edge_cases": "SKIP", "correctness": "FAIL"}
+    details = []
+    all_pass = True
+
+    def call(inputs):
+        with Timeout(timeout_s):
+            out = kernel_fn(**inputs)
+        if device.startswith("cuda"):
+            torch.cuda.synchronize()
+        return out
+
+    def tol_of(dt):
+        return tols.get(dt, {"atol": 1e-2, "rtol": 1e-2})
+
+    # stage 1: smoke
+    log("\n--- Stage 1: Smoke Test ---")
+    try:
+        inputs = gen(sizes[0][1], dtypes[0], device, seed=42)
+        expected = ref_fn(inputs)
+        out = call(inputs)
+        if has_nan_inf(out):
+            res["smoke_test"] = "FAIL"
+            details.append("  smoke: NaN/Inf in output")
+        else:
+            cmp = compare(out, expected, **tol_of(dtypes[0]))
+            res["smoke_test"] = "PASS" if cmp["match"] else "FAIL"
+            if not cmp["match"]:
+                details.append(f"  smoke: {cmp['reason']}")
+        log(f"  {res['smoke_test']}")
+    except BenchTimeoutError:
+        res["smoke_test"] = "FAIL"
+        details.append("  smoke: TIMEOUT")
+    except Exception as e:  # noqa: BLE001 - every failure is a verdict here
+        res["smoke_test"] = "FAIL"
+        details.append("  smoke: OOM" if _is_oom(e) else f"  smoke: CRASH ({type(e).__name__}: {e})")
+    if res["smoke_test"] == "FAIL":
+        res["details"] = details
+        log("\ncorrectness: FAIL (smoke test failed, aborting remaining stages)")
+        return res
+
+    # stage 2: shape sweep
+    log("\n--- Stage 2: Shape Sweep ---")
+    n_cfg = n_fail = 0
+    worst, worst_case = 0.0, ""
+    for label, sz in sizes:
+        for dt in dtypes:
+            n_cfg += 1
+            try:
+                inputs = gen(sz, dt, device, seed=42)
+                expected = ref_fn(inputs)
+                out = call(inputs)
+                if has_nan_inf(out):
+                    n_fail += 1
+                    details.append(f"  sweep {label}/{dt}: NaN/Inf")
+                    log(f"  FAIL: {label} {dt} -> NaN/Inf")
+                    continue
+                cmp = compare(out, expected, **tol_of(dt))
+                if cmp["max_abs_error"] > worst:
+                    worst, worst_case = cmp["max_abs_error"], f"{label}/{dt}"
+                if cmp["match"]:
+                    log(f"  PASS: {label} {dt} (max_err={cmp['max_abs_error']:.2e}, within_tol={cmp['pct_within_tol']:.1f}%)")
+                else:
+                    n_fail += 1
+                    details.append(f"  sweep {label}/{dt}: {cmp['reason']}")
+                    log(f"  FAIL: {label} {dt} -> {cmp['reason']}")
+            except BenchTimeoutError:
+                n_fail += 1
+                details.append(f"  sweep {label}/{dt}: TIMEOUT")
+                log(f"  FAIL: {label} {dt} -> TIMEOUT")
+            except Exception as e:  # noqa: BLE001
+                if _is_oom(e):
+                    log(f"  SKIP: {label} {dt} -> OOM")
+                else:
+                    n_fail += 1
+                    details.append(f"  sweep {label}/{dt}: {type(e).__name__}: {e}")
+                    log(f"  FAIL: {label} {dt} -> {type(e).__name__}: {e}")
+            finally:
+                _empty_cache(device)
+    if n_fail == 0:
+        res["shape_sweep"] = f"PASS ({n_cfg} configs, worst_err={worst:.2e} at {worst_case})"
+    else:
+        res["shape_sweep"] = f"FAIL ({n_fail}/{n_cfg} failed)"
+        all_pass = False
+    log(f"  shape_sweep: {res['shape_sweep']}")
+
+    if quick:
+        for k in ("numerical_stability", "determinism", "edge_cases"):
+            res[k] = "SKIP (quick mode)"
+        res["correctness"] = "PASS" if all_pass else "FAIL"
+        res["details"] = details
+        return res
+
+    # stage 3: numerical stability
+    log("\n--- Stage 3: Numerical Stability ---")
+    stab_ok = True
+    ssz, sdt = spec.stage_size(config), dtypes[0]
+    for case, _ in spec.ADVERSARIAL:
+        try:
+            inputs = spec.adversarial_inputs(gen(ssz, sdt, device, seed=42), case)
+            expected = ref_fn(inputs)
+            out = call(inputs)
+            o_bad, e_bad = has_nan_inf(out), has_nan_inf(expected)
+            if o_bad and not e_bad:
+                stab_ok = False
+                details.append(f"  stability {case}: NaN/Inf (reference is clean)")
+                log(f"  FAIL: {case} -> NaN/Inf (reference is clean)")
+            elif o_bad and e_bad:
+                log(f"  PASS: {case} -> both have NaN/Inf (expected overflow)")
+            else:
+                t = tol_of(sdt)
+                cmp = compare(out, expected, atol=10 * t["atol"], rtol=10 * t["rtol"])
+                if cmp["match"]:
+                    log(f"  PASS: {case} (max_err={cmp['max_abs_error']:.2e})")
+                else:
+                    stab_ok = False
+                    details.append(f"  stability {case}: {cmp['reason']}")
+                    log(f"  FAIL: {case} -> {cmp['reason']}")
+        except BenchTimeoutError:
+            stab_ok = False
+            details.append(f"  stability {case}: TIMEOUT")
+        except Exception as e:  # noqa: BLE001
+            if _is_oom(e):
+                log(f"  SKIP: {case} -> OOM")
+            else:
+                stab_ok = False
+                details.append(f"  stability {case}: {type(e).__name__}: {e}")
+        finally:
+            _empty_cache(device)
+    res["numerical_stability"] = "PASS" if stab_ok else "FAIL"
+    all_pass &= stab_ok
+
+    # stage 4: determinism
+    log("\n--- Stage 4: Determinism ---")
+    try:
+        outs = [call(gen(ssz, sdt, device, seed=42)) for _ in range(3)]
+        det_ok = all(torch.equal(outs[0], o) for o in outs[1:])
+        if not det_ok:
+            diff = max((outs[0].float() - o.float()).abs().max().item() for o in outs[1:])
+            details.append(f"  determinism: runs differ (max_diff={diff:.6e})")
+        res["determinism"] = "PASS" if det_ok else "FAIL"
+    except Exception as e:  # noqa: BLE001
+        det_ok = False
+        res["determinism"] = f"FAIL ({type(e).__name__})"
+        details.append(f"  determinism: {type(e).__name__}: {e}")
+    all_pass &= det_ok
+    log(f"  determinism: {res['determinism']}")
+
+    # stage 5: edge cases
+    log("\n--- Stage 5: Edge Cases ---")
+    edges = config.get("edge_sizes", [])
+    if not edges:
+        res["edge_cases"] = "SKIP (no edge sizes defined)"
+    else:
+        edge_ok = True
+        for label, sz in edges:
+            try:
+                inputs = gen(sz, dtypes[0], device, seed=42)
+                expected = ref_fn(inputs)
+                out = call(inputs)
+                if has_nan_inf(out) and not has_nan_inf(expected):
+                    edge_ok = False
+                    details.append(f"  edge {label}: NaN/Inf")
+                    continue
+                cmp = compare(out, expected, **tol_of(dtypes[0]))
+                if not cmp["match"]:
+                    edge_ok = False
+                    details.append(f"  edge {label}: {cmp['reason']}")
+                log(f"  {'PASS' if cmp['match'] else 'FAIL'}: {label} (max_err={cmp['max_abs_error']:.2e})")
+            except BenchTimeoutError:
+                edge_ok = False
+                details.append(f"  edge {label}: TIMEOUT")
+            except Exception as e:  # noqa: BLE001
+                if _is_oom(e):
+                    log(f"  SKIP: {label} -> OOM")
+                else:
+                    edge_ok = False
+                    details.append(f"  edge {label}: {type(e).__name__}: {e}")
+            finally:
+                _empty_cache(device)
+        res["edge_cases"] = "PASS" if edge_ok else "FAIL"
+        all_pass &= edge_ok
+    res["correctness"] = "PASS" if all_pass else "FAIL"
+    res["details"] = details
+    log(f"\ncorrectness: {res['correctness']}")
+    return res
+
+
+# ---------------------------------------------------------------------------------- timing
+_FLUSH: Dict[str, torch.Tensor] = {}
+
+
+def flush_cache(device: str = "cuda", mib: int = 512) -> None:
+    """Overwrite a buffer larger than the MI355X Infinity Cache (256 MB)."""
+    buf = _FLUSH.get(device)
+    if buf is None:
+        buf = _FLUSH[device] = torch.empty(mib * 2 ** 20, dtype=torch.uint8, device=device)
+    buf.zero_()
+
+
+def do_bench(fn: Callable, warmup_ms: float = 25.0, rep_ms: float = 100.0, flush: bool = True,
+             device: str = "cuda") -> Dict[str, float]:
+    """Event-timed calls of fn on the current stream with a cache clear before each call.
+
+    Call counts follow do_bench: estimate one call from 5, then ceil(warmup_ms / est) warm-up
+    and ceil(rep_ms / est) timed calls (at least 1 each). Returns mean / median / min in ms.
+    """
+    fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(5):
+        if flush:
+            flush_cache(device)
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    est = max(s.elapsed_time(e) / 5, 1e-3)
+    n_warm, n_rep = max(1, math.ceil(warmup_ms / est)), max(1, math.ceil(rep_ms / est))
+    for _ in range(n_warm):
+        fn()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_rep)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_rep)]
+    for i in range(n_rep):
+        if flush:
+            flush_cache(device)
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    t = sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
+    return {"mean": sum(t) / len(t), "median": t[len(t) // 2], "min": t[0], "n": n_rep}
+
+
+def roofline(flops: float, nbytes: float, ms: float, gpu: GPUSpec, dtype=None) -> dict:
+    """bench.py:1065-1082 classification; the compute peak follows the dtype (fp32 MFMA for fp32)."""
+    peak_c = gpu.peak_tflops_fp32 if dtype == torch.float32 else gpu.peak_tflops_fp16
+    tflops = flops / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
+    gbs = nbytes / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+    ai = flops / nbytes if nbytes else 0.0
+    ridge = (gpu.peak_tflops_fp16 * 1e12) / (gpu.peak_bandwidth_gb_s * 1e9) if gpu.peak_bandwidth_gb_s else 0.0
+    return {"throughput_tflops": tflops, "bandwidth_gb_s": gbs, "arithmetic_intensity": ai, "ridge_point": ridge,
+            "bottleneck": "memory_bound" if ai < ridge else "compute_bound",
+            "pct_peak_compute": 100.0 * tflops / peak_c if peak_c else 0.0,
+            "pct_peak_bandwidth": 100.0 * gbs / gpu.peak_bandwidth_gb_s if gpu.peak_bandwidth_gb_s else 0.0}
+
+
+def run_performance(kernel_fn: Callable, config: dict, gpu: GPUSpec, sizes_filter: str = "all",
+                    ref_fn: Optional[Callable] = None, device: str = "cuda", log=print) -> dict:
+    ref_fn = ref_fn or config["reference_fn"]
+    sizes = config["test_sizes"]
+    if sizes_filter == "all":
+        bench_sizes = sizes
+    else:
+        bench_sizes = [(l, s) for l, s in sizes if l == sizes_filter] or [spec.primary_size(config)]
+    primary_label, _ = spec.primary_size(config)
+    dt = config["test_dtypes"][0]
+    results, primary = [], None
+    for label, sz in bench_sizes:
+        try:
+            flops, nbytes = config["flops_fn"](sz), config["bytes_fn"](sz, dt)
+            inputs = config["input_generator"](sz, dt, device, seed=42)
+            k = do_bench(lambda: kernel_fn(**inputs), device=device)
+            r = do_bench(lambda: ref_fn(inputs), device=device)
+            rl = roofline(flops, nbytes, k["mean"], gpu, dt)
+            entry = {"label": label, "size": sz, "dtype": str(dt), "flops": flops, "bytes": nbytes,
+                     "kernel_latency_us": k["mean"] * 1e3, "kernel_median_us": k["median"] * 1e3,
+                     "pytorch_latency_us": r["mean"] * 1e3,
+                     "ref_throughput_tflops": flops / (r["mean"] * 1e-3) / 1e12,
+                     "speedup_vs_pytorch": r["mean"] / k["mean"], **rl}
+            results.append(entry)
+            if label == primary_label:
+                primary = entry
+            log(f"    {label}: kernel {entry['kernel_latency_us']:.2f} us | pytorch {entry['pytorch_latency_us']:.2f} us | "
+                f"speedup {entry['speedup_vs_pytorch']:.3f}x | {rl['throughput_tflops']:.3f} TFLOPS | "
+                f"{rl['bandwidth_gb_s']:.1f} GB/s")
+        except Exception as e:  # noqa: BLE001
+            log(f"    {'SKIP' if _is_oom(e) else 'ERROR'}: {label} -> {type(e).__name__}: {e}")
+        finally:
+            _empty_cache(device)
+    if primary is None and results:
+        primary = results[-1]
+    return {"primary": primary, "all": results}
+
+
+def run_profile(kernel_fn: Callable, config: dict, device: str = "cuda", trace_dir: str = "traces") -> str:
+    """torch.profiler trace of 10 calls at the 'medium' size (bench.py:1138-1187)."""
+    sz = next((s for l, s in config["test_sizes"] if l == "medium"), config["test_sizes"][0][1])
+    inputs = config["input_generator"](sz, config["test_dtypes"][0], device, seed=42)
+    os.makedirs(trace_dir, exist_ok=True)
+    acts = [torch.profiler.ProfilerActivity.CPU, torch.profiler.ProfilerActivity.CUDA]
+    with torch.profiler.profile(activities=acts, record_shapes=True) as prof:
+        for _ in range(5):
+            kernel_fn(**inputs)
+        torch.cuda.synchronize()
+        for _ in range(10):
+            kernel_fn(**inputs)
+        torch.cuda.synchronize()
+    path = os.path.join(trace_dir, "kernel_trace.json")
+    prof.export_chrome_trace(path)
+    print(prof.key_averages().table(sort_by="self_device_time_total", row_limit=20))
+    return path
+
+
+# ------------------------------------------------------------------------------ configs
+def kernel_configs() -> Dict[str, dict]:
+    """The op table with the stock-PyTorch baseline attached as each op's reference_fn."""
+    out = {}
+    for name, cfg in spec.KERNEL_CONFIGS.items():
+        c = dict(cfg)
+        c["reference_fn"] = baseline_torch.BASELINE[name]
+        out[name] = c
+    return out
+
+
+def _load_slot(kernel_type: Optional[str]):
+    """kernel_fn and KERNEL_TYPE: --kernel names one of ours; otherwise import kernel.py."""
+    if kernel_type is not None and kernel_type != "slot":
+        from . import kernels
+        return kernels.get(kernel_type), kernel_type
+    for p in (os.getcwd(), os.path.dirname(os.path.dirname(os.path.abspath(__file__)))):
+        if p not in sys.path:
+            sys.path.insert(0, p)
+    mod = importlib.import_module("kernel")
+    return mod.kernel_fn, getattr(mod, "KERNEL_TYPE")
+
+
+def main(argv=None) -> int:
+    t0 = time.time()
+    ap = argparse.ArgumentParser(description="libak355 per-op correctness and roofline harness")
+    ap.add_argument("--kernel", default=None, help="op name (default: kernel.py's KERNEL_TYPE)")
+    ap.add_argument("--sizes", default="all")
+    ap.add_argument("--quick", action="store_true")
+    ap.add_argument("--profile", action="store_true")
+    args = ap.parse_args(argv)
+    print("=" * 60 + "\nlibak355 kernel harness\n" + "=" * 60)
+    try:
+        kernel_fn, ktype = _load_slot(args.kernel)
+    except Exception as e:  # noqa: BLE001
+        print(f"\nERROR: failed to load the kernel: {type(e).__name__}: {e}")
+        traceback.print_exc()
+        print("\ncorrectness: FAIL\nthroughput_tflops: 0.000")
+        return 1
+    configs = kernel_configs()
+    if ktype not in configs:
+        print(f"\nERROR: unknown kernel type '{ktype}' (available: {', '.join(configs)})")
+        print("\ncorrectness: FAIL\nthroughput_tflops: 0.000")
+        return 1
+    cfg = configs[ktype]
+    gpu = detect_gpu()
+    print(f"kernel_type: {ktype}")
+    print("\n=== GPU INFO ===")
+    for k, v in vars(gpu).items():
+        print(f"gpu_{k}: {v}")
+    print("\n=== CORRECTNESS ===")
+    try:
+        corr = run_correctness(kernel_fn, cfg, quick=args.quick)
+    except Exception as e:  # noqa: BLE001
+        traceback.print_exc()
+        corr = {"correctness": "FAIL", "smoke_test": "CRASH"}
+    print("\n--- Correctness Summary ---")
+    for k in ("smoke_test", "shape_sweep", "numerical_stability", "determinism", "edge_cases", "correctness"):
+        print(f"{k}: {corr.get(k, 'N/A')}")
+    label, sz = spec.primary_size(cfg)
+    print(f"\n=== PERFORMANCE ({label}: {', '.join(f'{k}={v}' for k, v in sz.items())}, dtype={cfg['test_dtypes'][0]}) ===")
+    torch.cuda.reset_peak_memory_stats()
+    perf = run_performance(kernel_fn, cfg, gpu, "large" if args.quick else args.sizes)
+    vram = torch.cuda.max_memory_allocated() / 2 ** 20
+    p = perf["primary"]
+    if p:
+        print(f"\n--- Performance Summary (primary: {p['label']}) ---")
+        for k in ("kernel_latency_us", "kernel_median_us"):
+            print(f"{k.replace('kernel_', '')}: {p[k]:.2f}")
+        print(f"latency_ms: {p['kernel_latency_us'] / 1e3:.4f}")
+        print(f"throughput_tflops: {p['throughput_tflops']:.3f}")
+        print(f"bandwidth_gb_s: {p['bandwidth_gb_s']:.1f}")
+        print(f"pct_peak_compute: {p['pct_peak_compute']:.1f}%")
+        print(f"pct_peak_bandwidth: {p['pct_peak_bandwidth']:.1f}%")
+        print(f"arithmetic_intensity: {p['arithmetic_intensity']:.2f}")
+        print(f"ridge_point: {p['ridge_point']:.2f}")
+        print(f"bottleneck: {p['bottleneck']}")
+        print(f"flops: {p['flops']}\nbytes: {p['bytes']}\npeak_vram_mb: {vram:.1f}")
+        print("\n=== COMPARISON VS PYTORCH ===")
+        print(f"pytorch_latency_us: {p['pytorch_latency_us']:.2f}")
+        print(f"kernel_latency_us: {p['kernel_latency_us']:.2f}")
+        print(f"speedup_vs_pytorch: {p['speedup_vs_pytorch']:.3f}x")
+        print(f"pytorch_tflops: {p['ref_throughput_tflops']:.3f}\nkernel_tflops: {p['throughput_tflops']:.3f}")
+    if len(perf["all"]) > 1:
+        print("\n=== SIZE SWEEP ===")
+        print(f"{'size':<12} {'kernel_us':>12} {'pytorch_us':>12} {'speedup':>10} {'tflops':>10} {'GB/s':>10}")
+        for r in perf["all"]:
+            print(f"{r['label']:<12} {r['kernel_latency_us']:>12.2f} {r['pytorch_latency_us']:>12.2f} "
+                  f"{r['speedup_vs_pytorch']:>9.3f}x {r['throughput_tflops']:>10.3f} {r['bandwidth_gb_s']:>10.1f}")
+    if args.profile:
+        try:
+            print(f"profile_trace: {run_profile(kernel_fn, cfg)}")
+        except Exception as e:  # noqa: BLE001
+            print(f"\nWARNING: profiling failed: {type(e).__name__}: {e}")
+    print("\n=== FINAL ===")
+    print(f"kernel_type: {ktype}\ncorrectness: {corr['correctness']}")
+    print(f"throughput_tflops: {p['throughput_tflops'] if p else 0.0:.3f}")
+    print(f"speedup_vs_pytorch: {p['speedup_vs_pytorch'] if p else 0.0:.3f}x")
+    print(f"pct_peak_compute: {p['pct_peak_compute'] if p else 0.0:.1f}%")
+    print(f"bench_time_seconds: {time.time() - t0:.1f}")
+    return 0 if corr["correctness"] == "PASS" else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,383 @@
+"""Model plug-in verifier: the role of the reference's verify.py.
+
+    python -m autokernel_amd.verify [--model 7b|small|path/to/model.py --class-name C]
+        [--input-shape 1,2048] [--dtype float16] [--kernels all|matmul,rmsnorm,...]
+        [--atol 1e-2 --rtol 1e-2] [--diagnose] [--json out.json]
+
+Runs the stock forward, swaps modules for libak355-backed wrappers, reruns, compares the outputs
+(verify.py:687-765 semantics) and times both (10 warm-up, 50 timed, median; verify.py:258-307).
+
+Replacement strategies (the reference has matmul, layernorm and rmsnorm, verify.py:557-637;
+rotary embedding, attention and the SwiGLU MLP are added here):
+  matmul            every nn.Linear -> x @ W.T through ak_gemm reading W in place (no per-call
+                    weight.t().contiguous() copy, verify.py:429)
+  layernorm         nn.LayerNorm -> ak_layernorm
+  rmsnorm           RMSNorm-like modules (by class name, or weight + eps, no bias, "...norm") -> ak_rmsnorm
+  rotary_embedding  inside attention: RoPE through ak_rope_f32_tables
+  flash_attention   attention modules (wq / wk / wv / wo, n_heads, n_kv_heads) -> GQA-native
+                    ak_flash_attn_fwd on strided [B, T, H, D] views (no repeat_interleave, no
+                    transpose copies)
+  fused_mlp         SwiGLU feed-forward modules (w1 gate, w3 up, w2 down) -> ak_mlp_gate_up + ak_gemm
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+from typing import Any, Dict, Iterable, List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import kernels
+from .kernels import flash_attention as fa_mod
+from .kernels import rotary_embedding as rope_mod
+from .kernels.matmul import gemm
+
+ALL_KERNELS = ("matmul", "rmsnorm", "layernorm", "rotary_embedding", "flash_attention", "fused_mlp")
+WARMUP_RUNS = 10
+TIMED_RUNS = 50
+DEFAULT_TOLERANCES = {  # verify.py:51-55 (the north star asks 1e-2 for f16 / bf16 end to end)
+    torch.float16: {"atol": 1e-3, "rtol": 1e-3},
+    torch.bfloat16: {"atol": 2e-3, "rtol": 2e-3},
+    torch.float32: {"atol": 1e-5, "rtol": 1e-5},
+}
+RMSNORM_NAMES = {"RMSNorm", "LlamaRMSNorm", "T5LayerNorm", "GemmaRMSNorm"}
+
+
+# ------------------------------------------------------------------------------ wrappers
+def _linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    x2 = x.reshape(-1, x.shape[-1])
+    out = gemm(x2, weight.t())
+    if bias is not None:
+        out = out + bias
+    return out.view(*x.shape[:-1], weight.shape[0])
+
+
+class LinearWrapper(nn.Module):
+    """nn.Linear -> ak_gemm with the [out, in] weight read in place (b_trans = 1)."""
+
+    def __init__(self, original: nn.Linear):
+        super().__init__()
+        self.original = original
+        self.weight = original.weight
+        self.bias = original.bias
+
+    def forward(self, x):
+        return _linear(x, self.weight, self.bias)
+
+
+class LayerNormWrapper(nn.Module):
+    def __init__(self, original: nn.LayerNorm):
+        super().__init__()
+        self.original = original
+        self.weight, self.bias, self.eps = original.weight, original.bias, original.eps
+
+    def forward(self, x):
+        return kernels.get("layernorm")(x, self.weight, self.bias, self.eps)
+
+
+class RMSNormWrapper(nn.Module):
+    def __init__(self, original: nn.Module):
+        super().__init__()
+        self.original = original
+        self.weight = getattr(original, "weight", None)
+        self.eps = getattr(original, "eps", 1e-6)
+
+    def forward(self, x):
+        w = self.weight if self.weight is not None else torch.ones(x.shape[-1], device=x.device, dtype=x.dtype)
+        return kernels.get("rmsnorm")(x, w, self.eps)
+
+
+class FeedForwardWrapper(nn.Module):
+    """w2(silu(w1 x) * w3 x) -> fused gate/up kernel + down GEMM."""
+
+    def __init__(self, original: nn.Module, gate: nn.Linear, up: nn.Linear, down: nn.Linear):
+        super().__init__()
+        self.original = original
+        self.gate, self.up, self.down = gate, up, down
+
+    def forward(self, x):
+        return kernels.get("fused_mlp")(x, self.gate.weight, self.up.weight, self.down.weight, "silu")
+
+
+def _rope_tables_from(args) -> Tuple[torch.Tensor, torch.Tensor]:
+    """cos / sin from either (cos, sin) tensors or one complex freqs_cis tensor."""
+    if len(args) >= 2 and not torch.is_complex(args[0]):
+        return args[0], args[1]
+    f = args[0]
+    return f.real.float(), f.imag.float()
+
+
+class AttentionWrapper(nn.Module):
+    """GQA attention block (wq / wk / wv / wo) with libak355 RoPE and flash attention.
+
+    use_rope / use_fa select which of the two replace the stock steps; the projections use
+    ak_gemm when use_matmul is set.
+    """
+
+    def __init__(self, original: nn.Module, use_rope: bool, use_fa: bool, use_matmul: bool):
+        super().__init__()
+        self.original = original
+        self.use_rope, self.use_fa, self.use_matmul = use_rope, use_fa, use_matmul
+        o = original
+        self.n_heads, self.n_kv_heads, self.head_dim = o.n_heads, o.n_kv_heads, o.head_dim
+
+    def _proj(self, lin: nn.Linear, x):
+        return _linear(x, lin.weight, lin.bias) if self.use_matmul else lin(x)
+
+    def forward(self, x, *rope_args):
+        o = self.original
+        B, T, _ = x.shape
+        H, Hk, D = self.n_heads, self.n_kv_heads, self.head_dim
+        q = self._proj(o.wq, x).view(B, T, H, D)
+        k = self._proj(o.wk, x).view(B, T, Hk, D)
+        v = self._proj(o.wv, x).view(B, T, Hk, D)
+        cos, sin = _rope_tables_from(rope_args)
+        if self.use_rope:
+            q = rope_mod.apply_fp32_tables(q, cos, sin)
+            k = rope_mod.apply_fp32_tables(k, cos, sin)
+        else:
+            c, s = cos[:T].view(1, T, 1, -1), sin[:T].view(1, T, 1, -1)
+
+            def rot(t):
+                tf = t.float()
+                a, b = tf[..., 0::2], tf[..., 1::2]
+                return torch.stack((a * c - b * s, a * s + b * c), -1).flatten(-2).type_as(t)
+            q, k = rot(q), rot(k)
+        if self.use_fa:
+            y = torch.empty((B, T, H, D), device=x.device, dtype=x.dtype)
+            fa_mod.attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), True, None,
+                             out=y.transpose(1, 2))
+            y = y.view(B, T, H * D)
+        else:
+            qh, kh, vh = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+            if H != Hk:
+                kh = kh.repeat_interleave(H // Hk, dim=1)
+                vh = vh.repeat_interleave(H // Hk, dim=1)
+            y = F.scaled_dot_product_attention(qh, kh, vh, is_causal=True).transpose(1, 2).reshape(B, T, H * D)
+        return self._proj(o.wo, y)
+
+
+# ------------------------------------------------------------------------- module swapping
+def _is_rmsnorm(m: nn.Module) -> bool:
+    name = type(m).__name__
+    return name in RMSNORM_NAMES or (hasattr(m, "weight") and hasattr(m, "eps") and not hasattr(m, "bias")
+                                     and name.lower().endswith("norm") and not isinstance(m, nn.LayerNorm))
+
+
+def _is_attention(m: nn.Module) -> bool:
+    return all(hasattr(m, a) for a in ("wq", "wk", "wv", "wo", "n_heads", "n_kv_heads", "head_dim"))
+
+
+def _swiglu_parts(m: nn.Module):
+    for g, u, d in (("w1", "w3", "w2"), ("gate_proj", "up_proj", "down_proj")):
+        if all(isinstance(getattr(m, a, None), nn.Linear) for a in (g, u, d)):
+            return getattr(m, g), getattr(m, u), getattr(m, d)
+    return None
+
+
+class OptimizedModelContext:
+    """Swap modules for libak355 wrappers on enter, restore them on exit (verify.py:510-641)."""
+
+    def __init__(self, model: nn.Module, kernel_types: Iterable[str]):
+        self.model = model
+        self.kinds = set(kernel_types)
+        unknown = self.kinds - set(ALL_KERNELS)
+        if unknown:
+            raise ValueError(f"no replacement strategy for {sorted(unknown)}; known: {ALL_KERNELS}")
+        self._orig: Dict[str, nn.Module] = {}
+        self.applied: Dict[str, int] = {}
+
+    def _set(self, name: str, new: nn.Module) -> None:
+        parent = self.model
+        parts = name.split(".")
+        for p in parts[:-1]:
+            parent = getattr(parent, p)
+        self._orig[name] = getattr(parent, parts[-1])
+        setattr(parent, parts[-1], new)
+
+    def _count(self, kind):
+        self.applied[kind] = self.applied.get(kind, 0) + 1
+
+    def __enter__(self) -> nn.Module:
+        k = self.kinds
+        taken = set()
+        modules = list(self.model.named_modules())
+        # composite blocks first: their Linears are driven by the block wrapper
+        for name, m in modules:
+            if not name:
+                continue
+            if _is_attention(m) and (k & {"rotary_embedding", "flash_attention"}):
+                self._set(name, AttentionWrapper(m, "rotary_embedding" in k, "flash_attention" in k, "matmul" in k))
+                taken.update(n for n, _ in m.named_modules(prefix=name))
+                self._count("attention")
+            elif "fused_mlp" in k and _swiglu_parts(m) is not None and not isinstance(m, nn.Linear):
+                self._set(name, FeedForwardWrapper(m, *_swiglu_parts(m)))
+                taken.update(n for n, _ in m.named_modules(prefix=name))
+                self._count("fused_mlp")
+        for name, m in modules:
+            if not name or name in taken or any(name.startswith(t + ".") for t in taken):
+                continue
+            if "matmul" in k and isinstance(m, nn.Linear):
+                self._set(name, LinearWrapper(m))
+                self._count("matmul")
+            elif "layernorm" in k and isinstance(m, nn.LayerNorm):
+                self._set(name, LayerNormWrapper(m))
+                self._count("layernorm")
+            elif "rmsnorm" in k and _is_rmsnorm(m):
+                self._set(name, RMSNormWrapper(m))
+                self._count("rmsnorm")
+        return self.model
+
+    def __exit__(self, *exc):
+        for name in sorted(self._orig, key=lambda n: -n.count(".")):
+            parent = self.model
+            parts = name.split(".")
+            for p in parts[:-1]:
+                parent = getattr(parent, p)
+            setattr(parent, parts[-1], self._orig[name])
+        self._orig.clear()
+        return False
+
+
+# ---------------------------------------------------------------------- compare / timing
+def compare_outputs(ref: torch.Tensor, opt: torch.Tensor, dtype: torch.dtype,
+                    atol: Optional[float] = None, rtol: Optional[float] = None) -> Dict[str, Any]:
+    """verify.py:687-765: shape check, NaN / Inf asymmetry fails, allclose on the non-NaN part."""
+    r: Dict[str, Any] = {"shapes_match": ref.shape == opt.shape}
+    if not r["shapes_match"]:
+        r.update(correctness="FAIL", reason=f"shape mismatch {tuple(ref.shape)} vs {tuple(opt.shape)}")
+        return r
+    rf, of = ref.float(), opt.float()
+    r["ref_has_nan"], r["opt_has_nan"] = bool(torch.isnan(rf).any()), bool(torch.isnan(of).any())
+    r["ref_has_inf"], r["opt_has_inf"] = bool(torch.isinf(rf).any()), bool(torch.isinf(of).any())
+    if r["opt_has_nan"] and not r["ref_has_nan"]:
+        r.update(correctness="FAIL", reason="optimized output has NaN where the reference does not")
+        return r
+    if r["opt_has_inf"] and not r["ref_has_inf"]:
+        r.update(correctness="FAIL", reason="optimized output has Inf where the reference does not")
+        return r
+    valid = ~(torch.isnan(rf) & torch.isnan(of))
+    d = (rf - of).abs()[valid]
+    r["max_abs_error"] = float(d.max()) if d.numel() else 0.0
+    r["mean_abs_error"] = float(d.mean()) if d.numel() else 0.0
+    tol = DEFAULT_TOLERANCES.get(dtype, {"atol": 1e-4, "rtol": 1e-4})
+    atol = tol["atol"] if atol is None else atol
+    rtol = tol["rtol"] if rtol is None else rtol
+    ok = bool(torch.allclose(rf[valid], of[valid], atol=atol, rtol=rtol)) if valid.any() else True
+    r.update(correctness="PASS" if ok else "FAIL", atol=atol, rtol=rtol)
+    if not ok:
+        r["reason"] = f"values exceed tolerance (atol={atol}, rtol={rtol}); max_abs_error={r['max_abs_error']:.6e}"
+    return r
+
+
+def make_token_ids(model: nn.Module, shape: Tuple[int, ...], device, seed: int = 42) -> torch.Tensor:
+    """Token ids uniform in [0, vocab) from a seeded CPU generator (verify.py:230-251 draws 32000)."""
+    vocab = 32000
+    for m in model.modules():
+        if isinstance(m, nn.Embedding):
+            vocab = m.num_embeddings
+            break
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, vocab, shape, generator=g, dtype=torch.long).to(device)
+
+
+@torch.no_grad()
+def benchmark_model(model: nn.Module, inp, warmup: int = WARMUP_RUNS, timed: int = TIMED_RUNS):
+    """(output, median ms) over `timed` event-timed forwards after `warmup` (verify.py:258-307)."""
+    run = (lambda: model(**inp)) if isinstance(inp, dict) else (lambda: model(inp))
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    st = [torch.cuda.Event(enable_timing=True) for _ in range(timed)]
+    en = [torch.cuda.Event(enable_timing=True) for _ in range(timed)]
+    for i in range(timed):
+        st[i].record()
+        run()
+        en[i].record()
+    torch.cuda.synchronize()
+    t = sorted(a.elapsed_time(b) for a, b in zip(st, en))
+    out = run()
+    torch.cuda.synchronize()
+    if not isinstance(out, torch.Tensor):
+        out = out[0] if isinstance(out, (tuple, list)) else out
+    return out, t[len(t) // 2]
+
+
+def diagnose(model, inp, ref_out, kinds: List[str], dtype, atol=None, rtol=None) -> List[dict]:
+    """Apply one kernel type at a time to find which one breaks the comparison (verify.py:772-828)."""
+    rows = []
+    for kind in kinds:
+        with OptimizedModelContext(model, [kind]) as m, torch.no_grad():
+            out = m(inp)
+        torch.cuda.synchronize()
+        c = compare_outputs(ref_out, out, dtype, atol, rtol)
+        rows.append({"kernel_type": kind, "correctness": c["correctness"], "max_abs_error": c.get("max_abs_error")})
+    return rows
+
+
+def _load_model(args, dtype, device) -> nn.Module:
+    from . import llama
+    if args.model in ("7b", "small"):
+        return llama.build(args.model, dtype, device, seed=args.seed, n_layers=args.layers)
+    spec_ = importlib.util.spec_from_file_location("user_model", os.path.abspath(args.model))
+    mod = importlib.util.module_from_spec(spec_)
+    spec_.loader.exec_module(mod)
+    with torch.device(device):
+        model = getattr(mod, args.class_name)().to(dtype)
+    return model.eval()
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="libak355 model plug-in verifier")
+    ap.add_argument("--model", default="7b", help="7b, small, or a model .py file")
+    ap.add_argument("--class-name", default="LlamaModel7B")
+    ap.add_argument("--input-shape", default="1,2048")
+    ap.add_argument("--dtype", default="float16", choices=["float16", "bfloat16", "float32"])
+    ap.add_argument("--kernels", default="all")
+    ap.add_argument("--layers", type=int, default=None, help="override the layer count (7b / small)")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--atol", type=float, default=None)
+    ap.add_argument("--rtol", type=float, default=None)
+    ap.add_argument("--warmup", type=int, default=WARMUP_RUNS)
+    ap.add_argument("--timed", type=int, default=TIMED_RUNS)
+    ap.add_argument("--diagnose", action="store_true")
+    ap.add_argument("--json", default=None)
+    args = ap.parse_args(argv)
+    dtype = getattr(torch, args.dtype)
+    dev = torch.device("cuda:0")
+    kinds = list(ALL_KERNELS) if args.kernels == "all" else [s.strip() for s in args.kernels.split(",")]
+    model = _load_model(args, dtype, dev)
+    shape = tuple(int(s) for s in args.input_shape.split(","))
+    inp = make_token_ids(model, shape, dev)
+    print(f"model: {type(model).__name__}, params {sum(p.numel() for p in model.parameters()) / 1e9:.2f} B, "
+          f"input {list(shape)}, dtype {args.dtype}")
+    ref_out, ref_ms = benchmark_model(model, inp, args.warmup, args.timed)
+    ctx = OptimizedModelContext(model, kinds)
+    with ctx as m:
+        opt_out, opt_ms = benchmark_model(m, inp, args.warmup, args.timed)
+        applied = dict(ctx.applied)
+    cmp = compare_outputs(ref_out, opt_out, dtype, args.atol, args.rtol)
+    res = {"model": type(model).__name__, "input_shape": list(shape), "dtype": args.dtype, "kernels": kinds,
+           "replaced": applied, "ref_latency_ms": ref_ms, "opt_latency_ms": opt_ms,
+           "end_to_end_speedup": ref_ms / opt_ms, **{k: v for k, v in cmp.items()}}
+    if args.diagnose and cmp["correctness"] != "PASS":
+        res["diagnosis"] = diagnose(model, inp, ref_out, kinds, dtype, args.atol, args.rtol)
+    for k in ("replaced", "ref_latency_ms", "opt_latency_ms", "end_to_end_speedup", "max_abs_error",
+              "mean_abs_error", "correctness"):
+        print(f"{k}: {res.get(k)}")
+    if "diagnosis" in res:
+        for d in res["diagnosis"]:
+            print(f"  {d}")
+    if args.json:
+        with open(args.json, "w") as f:
+            json.dump(res, f, indent=2, default=str)
+    return 0 if cmp["correctness"] == "PASS" else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

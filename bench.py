@@ -1,0 +1,256 @@
+#!/usr/bin/env python3
+"""Benchmark of the libak355 nine-op suite on one MI355X; prints ONE JSON line on stdout.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-ops] [--no-e2e] [--cpu-seconds 10]
+
+Headline workload (the configuration its metric is quoted on that is
+not the reference's CPU case): one step = rotary embedding of q and k, f16 [1, 32, 2048, 128]
+with theta-10000 tables for positions 0..2047, then a row softmax of f16 [8192, 8192] ~N(0, 3).
+Inputs are resident in HBM before timing; K steps are timed between device synchronisations.
+`value` is the step's algorithmic bytes (reads + writes of the three ops) per second.
+
+Also reported (same JSON line):
+  roofline      the dominant kernel (the softmax, 80 % of a step's bytes): algorithmic bytes per
+                launch over its average launch time from HIP events recorded on its stream inside
+                the timed region; traffic = HBM bytes per launch measured with rocprofv3 PMC
+                counters (profiles/traffic.json), or null when not measured.
+  cpu_baseline  the CPU oracle (a restatement of the reference's reference.py on PyTorch CPU)
+                on a bounded sample of the same step, timed on this host.
+  ops           every BASELINE workload (rmsnorm, rope, softmax, matmul, fused MLP, attention)
+                and the reference harness's primary sizes of layernorm / cross-entropy / reduce,
+                cold-cache timed (cache cleared before each call), vs stock PyTorch-ROCm.
+  e2e           LLaMA-7B-shaped forward [1, 2048] f16, stock PyTorch vs all ops swapped.
+Progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "per-op TFLOPS or GB/s as % of MI355X roofline; LLaMA-7B fwd latency ms"
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2516.6
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def headline(steps: int, warmup: int):
+    import torch
+    from autokernel_amd import kernels, spec
+    dev = torch.device("cuda:0")
+    r = spec.baseline_rope(device=dev)
+    s = spec.baseline_softmax(device=dev)
+    rope, softmax = kernels.get("rotary_embedding"), kernels.get("softmax")
+    q, k, cos, sin, x = r["q"], r["k"], r["cos"], r["sin"], s["x"]
+    rope_bytes = (2 * q.numel() + 2 * cos.numel()) * 2  # x in, y out, cos + sin tables (f16)
+    sm_bytes = 2 * x.numel() * 2
+    step_bytes = 2 * rope_bytes + sm_bytes
+
+    def step(ev=None):
+        rope(q, cos, sin)
+        rope(k, cos, sin)
+        if ev is not None:
+            ev[0].record()
+        softmax(x)
+        if ev is not None:
+            ev[1].record()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter()
+    t0.record()
+    for i in range(steps):
+        step(evs[i])
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall
+    ms_total = t0.elapsed_time(t1)
+    sm_ms = sum(a.elapsed_time(b) for a, b in evs) / steps
+    return {"ms_per_step": ms_total / steps, "wall_s": wall, "step_bytes": step_bytes,
+            "softmax_ms": sm_ms, "softmax_bytes": sm_bytes, "rope_bytes": rope_bytes}
+
+
+def traffic_for(key: str):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f).get(key)
+        return None if t is None else int(t["hbm_bytes_per_launch"])
+    except (OSError, ValueError, KeyError, TypeError):
+        return None
+
+
+def op_table():
+    """Cold-cache timing of every BASELINE workload and the harness's primary extras."""
+    import torch
+    from autokernel_amd import baseline_torch as BT
+    from autokernel_amd import harness, kernels, spec
+    dev = torch.device("cuda:0")
+    K = kernels.get
+    rows = []
+
+    def add(name, unit, work, fn, ref, note=""):
+        t = harness.do_bench(fn)
+        tr = harness.do_bench(ref)
+        rate = work / (t["median"] * 1e-3) / (1e9 if unit == "GB/s" else 1e12)
+        peak = HBM_PEAK_GBS if unit == "GB/s" else MFMA_PEAK_TFLOPS
+        row = {"op": name, "median_us": round(t["median"] * 1e3, 2), "mean_us": round(t["mean"] * 1e3, 2),
+               "achieved": round(rate, 1), "unit": unit, "peak": peak, "frac": round(rate / peak, 4),
+               "torch_median_us": round(tr["median"] * 1e3, 2),
+               "speedup_vs_torch": round(tr["median"] / t["median"], 3)}
+        if note:
+            row["note"] = note
+        rows.append(row)
+        log(f"  {name:44s} {row['median_us']:9.1f} us  {rate:8.1f} {unit}  {100 * rate / peak:5.1f}%  "
+            f"torch {row['torch_median_us']:9.1f} us  x{row['speedup_vs_torch']}")
+        torch.cuda.empty_cache()
+
+    i = spec.baseline_rmsnorm(device=dev)
+    add("rmsnorm f16 [4096,4096] (C1)", "GB/s", (2 * 4096 * 4096 + 4096) * 2,
+        lambda: K("rmsnorm")(i["x"], i["weight"], 1e-6), lambda: BT.rmsnorm(i["x"], i["weight"], 1e-6))
+    r = spec.baseline_rope(device=dev)
+    add("rotary_embedding f16 q [1,32,2048,128] (C2a)", "GB/s", (2 * r["q"].numel() + 2 * r["cos"].numel()) * 2,
+        lambda: K("rotary_embedding")(r["q"], r["cos"], r["sin"]), lambda: BT.rotary_embedding(r["q"], r["cos"], r["sin"]))
+    s = spec.baseline_softmax(device=dev)
+    add("softmax f16 [8192,8192] (C2b)", "GB/s", 2 * s["x"].numel() * 2,
+        lambda: K("softmax")(s["x"]), lambda: BT.softmax(s["x"]))
+    del i, r, s
+    m = spec.baseline_matmul(device=dev)
+    add("matmul bf16 4096^3 (C3a)", "TFLOP/s", 2 * 4096 ** 3,
+        lambda: K("matmul")(m["A"], m["B"]), lambda: BT.matmul(m["A"], m["B"]))
+    del m
+    f = spec.baseline_fused_mlp(device=dev)
+    add("fused_mlp bf16 x[2048,4096] H=11008 (C3b)", "TFLOP/s", 2 * 2048 * 4096 * 11008 * 3,
+        lambda: K("fused_mlp")(**f), lambda: BT.fused_mlp(**f))
+    del f
+    for B, S in ((4, 2048), (1, 8192)):
+        a = spec.baseline_attention(device=dev, B=B, S=S)
+        sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(a["Q"], a["K"], a["V"], is_causal=True)
+        add(f"flash_attention f16 causal [{B},32,{S},128] (C4)", "TFLOP/s", spec.attention_causal_flops(B, 32, S, 128),
+            lambda: K("flash_attention")(**a), sdpa, note="causal flop count; torch = SDPA")
+        del a
+    x = torch.randn(4096, 2048, device=dev, dtype=torch.float16)
+    w, b = torch.ones(2048, device=dev, dtype=torch.float16), torch.zeros(2048, device=dev, dtype=torch.float16)
+    add("layernorm f16 [4096,2048] (harness large)", "GB/s", (2 * 4096 * 2048 + 2 * 2048) * 2,
+        lambda: K("layernorm")(x, w, b), lambda: BT.layernorm(x, w, b))
+    ce = spec.gen_cross_entropy({"batch": 4096, "vocab": 32000}, torch.float16, dev)
+    add("cross_entropy f16 [4096,32000] (harness large)", "GB/s", (4096 * 32000 + 4096) * 2,
+        lambda: K("cross_entropy")(**ce), lambda: BT.cross_entropy(**ce))
+    xr = spec.gen_reduce({"M": 8192, "N": 8192}, torch.float16, dev)["x"]
+    add("reduce sum f16 [8192,8192] (harness large)", "GB/s", (8192 * 8192 + 8192) * 2,
+        lambda: K("reduce")(xr), lambda: BT.reduce_sum(xr))
+    return rows
+
+
+def e2e(timed: int = 20, warm: int = 3):
+    import torch
+    from autokernel_amd import llama, verify
+    dev = torch.device("cuda:0")
+    model = llama.build("7b", torch.float16, dev)
+    ids = verify.make_token_ids(model, (1, 2048), dev)
+    ref_out, ref_ms = verify.benchmark_model(model, ids, warm, timed)
+    with verify.OptimizedModelContext(model, verify.ALL_KERNELS) as m:
+        opt_out, opt_ms = verify.benchmark_model(m, ids, warm, timed)
+    cmp = verify.compare_outputs(ref_out, opt_out, torch.float16, 1e-2, 1e-2)
+    res = {"model": "LlamaModel7B (GQA 32/8 heads, FFN 11008, vocab 32000), random N(0,0.02) init",
+           "input": [1, 2048], "dtype": "f16", "torch_ms": round(ref_ms, 3), "ak_ms": round(opt_ms, 3),
+           "speedup": round(ref_ms / opt_ms, 3), "correctness_1e-2": cmp["correctness"],
+           "max_abs_error": cmp.get("max_abs_error")}
+    del model
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(seconds: float):
+    """The CPU oracle on a bounded sample of one step: 4 of 32 heads of q and k, 1024 of 8192 rows."""
+    import torch
+    from autokernel_amd import spec
+    from oracle import reference_ops as R
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    r = spec.baseline_rope(H=4)
+    s = spec.baseline_softmax(R=1024)
+    sample_bytes = 2 * (2 * r["q"].numel() + 2 * r["cos"].numel()) * 2 + 2 * s["x"].numel() * 2
+
+    def step():
+        R.rotary_embedding_ref(r["q"], r["cos"], r["sin"])
+        R.rotary_embedding_ref(r["k"], r["cos"], r["sin"])
+        R.softmax_ref(s["x"])
+
+    step()
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        step()
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return {"value": round(sample_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"1/8 of a step (rope q,k on 4 of 32 heads; softmax on 1024 of 8192 rows), "
+                                      f"{n} reps in {n * dt:.1f}s, oracle.reference_ops on PyTorch CPU"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-ops", action="store_true", help="skip the per-op table")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the LLaMA-7B forward")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the path has no cross-GPU work", file=sys.stderr)
+        return 2
+    import torch
+    from autokernel_amd import _lib
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    log(f"libak355 {_lib.version()} on {torch.cuda.get_device_properties(0).gcnArchName}")
+    h = headline(args.steps, args.warmup)
+    value = h["step_bytes"] / (h["ms_per_step"] * 1e-3) / 1e9
+    sm_gbs = h["softmax_bytes"] / (h["softmax_ms"] * 1e-3) / 1e9
+    log(f"headline: {h['ms_per_step'] * 1e3:.1f} us/step, {value:.1f} GB/s; softmax {h['softmax_ms'] * 1e3:.1f} us, {sm_gbs:.1f} GB/s")
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(h["ms_per_step"], 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "BASELINE configs[1]: rotary_embedding f16 q,k [1,32,2048,128] (theta 10000, "
+                               "positions 0..2047) + softmax f16 [8192,8192] ~N(0,3), one pass each per step",
+                   "step_bytes": h["step_bytes"], "parallelism": "single GPU"},
+        "roofline": {"kernel": "softmax f16 [8192,8192]", "bound": "hbm", "achieved": round(sm_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(sm_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_for("softmax_f16_8192x8192"),
+                     "algorithmic_bytes": h["softmax_bytes"], "avg_launch_us": round(h["softmax_ms"] * 1e3, 2)},
+    }
+    if not args.no_ops:
+        log("per-op table (cold cache):")
+        out["ops"] = op_table()
+    if not args.no_e2e:
+        try:
+            log("LLaMA-7B forward:")
+            out["e2e"] = e2e()
+            log(f"  {out['e2e']}")
+        except Exception as e:  # noqa: BLE001 - report, keep the headline
+            out["e2e"] = {"error": f"{type(e).__name__}: {e}"}
+    if args.cpu_seconds > 0:
+        log("cpu baseline:")
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

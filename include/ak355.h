@@ -87,6 +87,16 @@ int ak_rope(int dtype, const void* x, const void* cos_t, const void* sin_t, void
             hipStream_t stream);
 
 /*
+ * Rotary embedding in the form a LLaMA block applies it: x (f16 / bf16) rotated by fp32 tables
+ * with fp32 arithmetic and one rounding to x's dtype; cos_t, sin_t: fp32 [table_rows, head_dim/2];
+ * same row-to-table mapping as ak_rope. head_dim a multiple of 8, 16-byte aligned x and y.
+ * Replaces: models/llama_7b.py:40-48 apply_rotary_emb (complex multiply in fp32, type_as(x)).
+ */
+int ak_rope_f32_tables(int dtype, const void* x, const float* cos_t, const float* sin_t, void* y,
+                       int64_t rows, int64_t head_dim, int64_t table_rows, int64_t rep_inner,
+                       hipStream_t stream);
+
+/*
  * Mean cross-entropy over rows: out = mean_r( logsumexp(x_r) - x_r[t_r] ), rows whose target is
  * ignore_index excluded from sum and count (F.cross_entropy semantics). A target outside
  * [0, vocab) that is not ignore_index makes the result NaN.

@@ -14,10 +14,23 @@ def _cpu(*ts):
     return [t.detach().cpu() if isinstance(t, torch.Tensor) else t for t in ts]
 
 
+def _mm(a, b):
+    """torch.matmul with the reference's arithmetic: exact products summed in fp32 or wider, one
+    rounding to the input dtype. f16 / bf16 operands are multiplied in fp32 and rounded (what the
+    GPU BLAS path computes; CPU f16 GEMM is much slower); fp32 operands are multiplied in fp64 and
+    rounded once, i.e. the correctly rounded product, so the oracle's own summation error does not
+    eat into the 1e-4 fp32 tolerance."""
+    if a.dtype in (torch.float16, torch.bfloat16) and b.dtype == a.dtype:
+        return torch.matmul(a.float(), b.float()).to(a.dtype)
+    if a.dtype == torch.float32 and b.dtype == torch.float32:
+        return torch.matmul(a.double(), b.double()).float()
+    return torch.matmul(a, b)
+
+
 def matmul_ref(A, B):
     """reference.py:10-12 -- torch.matmul(A, B)."""
     A, B = _cpu(A, B)
-    return torch.matmul(A, B)
+    return _mm(A, B)
 
 
 def softmax_ref(x, dim=-1):
@@ -45,26 +58,26 @@ def flash_attention_ref(Q, K, V, causal=True, sm_scale=None):
     Q, K, V = _cpu(Q, K, V)
     if sm_scale is None:
         sm_scale = Q.shape[-1] ** -0.5
-    scores = torch.matmul(Q, K.transpose(-2, -1)) * sm_scale
+    scores = _mm(Q, K.transpose(-2, -1)) * sm_scale
     if causal:
         sq, sk = Q.shape[-2], K.shape[-2]
         upper = torch.triu(torch.ones(sq, sk, dtype=torch.bool), diagonal=1)
         scores = scores.masked_fill(upper, float("-inf"))
-    return torch.matmul(F.softmax(scores, dim=-1), V)
+    return _mm(F.softmax(scores, dim=-1), V)
 
 
 def fused_mlp_ref(x, w_gate, w_up, w_down, activation="silu"):
     """reference.py:45-55 -- act(x @ w_gate.T) * (x @ w_up.T) @ w_down.T, each step materialised."""
     x, w_gate, w_up, w_down = _cpu(x, w_gate, w_up, w_down)
-    g = x @ w_gate.T
-    u = x @ w_up.T
+    g = _mm(x, w_gate.T)
+    u = _mm(x, w_up.T)
     if activation == "silu":
         g = F.silu(g)
     elif activation == "gelu":
         g = F.gelu(g)
     elif activation == "relu2":
         g = F.relu(g) ** 2
-    return (g * u) @ w_down.T
+    return _mm(g * u, w_down.T)
 
 
 def cross_entropy_ref(logits, targets):

@@ -1,0 +1,48 @@
+"""Module swapping of the plug-in verifier on a tiny LLaMA (CPU: structure only, no forward)."""
+from __future__ import annotations
+
+import torch.nn as nn
+
+from autokernel_amd import llama, verify
+
+
+def tiny():
+    return llama.LlamaModel(vocab_size=100, dim=128, n_layers=2, n_heads=2, n_kv_heads=1, hidden_dim=256, max_seq_len=16)
+
+
+def test_all_strategies_apply_and_restore():
+    m = tiny()
+    before = {n: type(x) for n, x in m.named_modules()}
+    ctx = verify.OptimizedModelContext(m, verify.ALL_KERNELS)
+    with ctx as pm:
+        assert ctx.applied == {"attention": 2, "fused_mlp": 2, "matmul": 1, "rmsnorm": 5}
+        assert isinstance(pm.layers[0].attention, verify.AttentionWrapper)
+        assert isinstance(pm.layers[1].feed_forward, verify.FeedForwardWrapper)
+        assert isinstance(pm.output, verify.LinearWrapper)
+        assert isinstance(pm.norm, verify.RMSNormWrapper)
+    assert {n: type(x) for n, x in m.named_modules()} == before
+
+
+def test_matmul_only_swaps_every_linear():
+    m = tiny()
+    ctx = verify.OptimizedModelContext(m, ["matmul"])
+    with ctx:
+        assert ctx.applied == {"matmul": 2 * 7 + 1}
+        assert all(not isinstance(x, nn.Linear) or n.endswith(".original") for n, x in m.named_modules())
+
+
+def test_unknown_strategy_rejected():
+    import pytest
+    with pytest.raises(ValueError):
+        verify.OptimizedModelContext(tiny(), ["conv2d"])
+
+
+def test_compare_outputs_rules():
+    import torch
+    a = torch.randn(4, 8)
+    assert verify.compare_outputs(a, a.clone(), torch.float32)["correctness"] == "PASS"
+    b = a.clone()
+    b[0, 0] = float("nan")
+    assert verify.compare_outputs(a, b, torch.float32)["correctness"] == "FAIL"
+    assert verify.compare_outputs(b, b.clone(), torch.float32)["correctness"] == "PASS"  # NaN in both
+    assert verify.compare_outputs(a, a + 1, torch.float32, 1e-2, 1e-2)["correctness"] == "FAIL"
