@@ -7,12 +7,13 @@ There is no fallback: if the library is missing or a launch fails, the caller ge
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().with_name("libak355.so")
+LIB_PATH = Path(os.environ.get("AK355_LIB") or Path(__file__).resolve().with_name("libak355.so"))
 
 AK_F32, AK_F16, AK_BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: AK_F32, torch.float16: AK_F16, torch.bfloat16: AK_BF16}

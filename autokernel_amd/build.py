@@ -57,10 +57,25 @@ def _compile(src: Path, extra: list[str]) -> tuple[Path, str]:
     return obj, msgs
 
 
-def build(verbose: bool = True, jobs: int | None = None, extra_flags: list[str] | None = None) -> Path:
-    """Compile every HIP source for gfx950 and link ``libak355.so``. Always rebuilds."""
+def build(verbose: bool = True, jobs: int | None = None, extra_flags: list[str] | None = None,
+          out: Path | None = None, build_dir: Path | None = None) -> Path:
+    """Compile every HIP source for gfx950 and link ``libak355.so``. Always rebuilds.
+
+    extra_flags / out / build_dir produce a variant library elsewhere (tuning builds)."""
+    global BUILD_DIR
     t0 = time.time()
-    BUILD_DIR.mkdir(exist_ok=True)
+    lib_path = Path(out) if out else LIB_PATH
+    saved = BUILD_DIR
+    if build_dir:
+        BUILD_DIR = Path(build_dir)
+    try:
+        return _build(verbose, jobs, extra_flags, lib_path, t0)
+    finally:
+        BUILD_DIR = saved
+
+
+def _build(verbose, jobs, extra_flags, lib_path: Path, t0: float) -> Path:
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
@@ -74,15 +89,15 @@ def build(verbose: bool = True, jobs: int | None = None, extra_flags: list[str] 
             objs.append(obj)
             if verbose and msgs.strip():
                 print(msgs, file=sys.stderr)
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+    tmp = lib_path.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, sorted(objs))]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib_path)
     if verbose:
-        print(f"built {LIB_PATH} from {len(srcs)} sources in {time.time() - t0:.1f}s")
-    return LIB_PATH
+        print(f"built {lib_path} from {len(srcs)} sources in {time.time() - t0:.1f}s")
+    return lib_path
 
 
 if __name__ == "__main__":

@@ -301,6 +301,14 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma(
 // --------------------------------------------------------------------------------------------
 constexpr int kF32BM = 128, kF32BN = 128, kF32BK = 16;
 
+// s += v with the lost low-order bits kept in c (Kahan). No multiplies, so no contraction applies.
+__device__ __forceinline__ void kahan_add(float& s, float& c, float v) {
+  const float y = v - c;
+  const float t = s + y;
+  c = (t - s) - y;
+  s = t;
+}
+
 template <bool BT>
 __global__ __launch_bounds__(256) void gemm_f32(const float* __restrict__ A, const float* __restrict__ B,
                                                 float* __restrict__ C, int M, int N, int K,
@@ -345,11 +353,11 @@ __global__ __launch_bounds__(256) void gemm_f32(const float* __restrict__ A, con
       else sB[st][(e / BN) * PBN + e % BN] = rb[i];
     }
   };
-  f32x4 acc[4][4];
+  f32x4 acc[4][4], comp[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j) acc[i][j] = comp[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int KT = (K + BK - 1) / BK;
   gload(0);
   sstore(0);
@@ -381,10 +389,14 @@ __global__ __launch_bounds__(256) void gemm_f32(const float* __restrict__ A, con
 #pragma unroll
         for (int j = 0; j < 4; ++j) part[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fb[j], fa[i], part[i][j], 0, 0, 0);
     }
+    // Kahan-compensated outer sum over k-tiles: the running total's rounding error is carried
+    // in `comp` and fed back, so long K (8192+) stays within the fp32 tolerance.
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] += part[i][j];
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kahan_add(acc[i][j][e], comp[i][j][e], part[i][j][e]);
     if (kt + 1 < KT) sstore(cur ^ 1);
     __syncthreads();
   }
@@ -442,13 +454,20 @@ static void launch_gemm_cfg(const void* A, const void* B0, const void* B1, void*
       ldc, tiles_m, tiles_n);
 }
 
+// Waves along N of the 256x256 tile: 4 (8 waves of 128x64) or 2 (4 waves of 128x128, one wave
+// per SIMD, accumulators in AGPRs).
+#ifndef AK_GEMM_BIG_WN
+#define AK_GEMM_BIG_WN 4
+#endif
+constexpr int kBigWN = AK_GEMM_BIG_WN;
+
 template <typename T, bool BT, bool VEC, int NB, int EPI>
 static void launch_gemm_tiled(const void* A, const void* B0, const void* B1, void* C, int M, int N,
                               int K, int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
   const TileCfg t = pick_tile(M, N, NB);
   if constexpr (NB == 1) {
     if (t.bm == 256 && t.bn == 256)
-      launch_gemm_cfg<T, BT, VEC, 256, 256, 2, 4, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+      launch_gemm_cfg<T, BT, VEC, 256, 256, 2, kBigWN, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
     else if (t.bm == 256)
       launch_gemm_cfg<T, BT, VEC, 256, 128, 4, 2, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
     else
@@ -513,11 +532,11 @@ __global__ __launch_bounds__(256) void gate_up_f32(const float* __restrict__ X, 
   const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
   const int wm = wid >> 1, wn = wid & 1;
   const int fr = lane & 15, fk = lane >> 4;
-  f32x4 ag[2][2], au[2][2];
+  f32x4 ag[2][2], au[2][2], cg[2][2], cu[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) ag[i][j] = au[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 2; ++j) ag[i][j] = au[i][j] = cg[i][j] = cu[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int k0 = 0; k0 < D; k0 += BK) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -556,10 +575,12 @@ __global__ __launch_bounds__(256) void gate_up_f32(const float* __restrict__ X, 
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        ag[i][j] += pg[i][j];
-        au[i][j] += pu[i][j];
-      }
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          kahan_add(ag[i][j][e], cg[i][j][e], pg[i][j][e]);
+          kahan_add(au[i][j][e], cu[i][j][e], pu[i][j][e]);
+        }
     __syncthreads();
   }
 #pragma unroll

@@ -80,10 +80,23 @@ def fused_mlp_ref(x, w_gate, w_up, w_down, activation="silu"):
     return _mm(g * u, w_down.T)
 
 
-def cross_entropy_ref(logits, targets):
-    """reference.py:58-60 -- F.cross_entropy(logits.view(-1, V), targets.view(-1))."""
+def cross_entropy_ref(logits, targets, ignore_index=-100):
+    """reference.py:58-60 -- F.cross_entropy(logits.view(-1, V), targets.view(-1)).
+
+    For f16 / bf16 this spells out the arithmetic of the GPU run the reference harness makes:
+    log_softmax stored in the logits' dtype, -logp[target] summed in fp32 over the rows whose
+    target is not ignore_index, divided by their count, rounded once. (PyTorch's CPU kernel sums
+    the half values in half and overflows once the sum passes 65504, e.g. 8192 rows of ~10.8.)
+    """
     logits, targets = _cpu(logits, targets)
-    return F.cross_entropy(logits.view(-1, logits.size(-1)), targets.view(-1))
+    x = logits.view(-1, logits.size(-1))
+    t = targets.view(-1)
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        return F.cross_entropy(x, t, ignore_index=ignore_index)
+    lp = F.log_softmax(x, dim=-1)
+    keep = t != ignore_index
+    picked = -lp.gather(1, t.clamp_min(0).unsqueeze(1)).squeeze(1).float()
+    return (picked[keep].sum() / keep.sum()).to(x.dtype)
 
 
 def rotary_embedding_ref(x, cos, sin):
