@@ -30,6 +30,11 @@ constexpr int kKC = kBK / 8;      // 16-byte chunks per tile row
 __device__ __forceinline__ int swz(int row, int c) { return c ^ ((row ^ (row >> 3)) & 7); }
 // element offset of chunk c of row `row` in a [rows][64] tile
 __device__ __forceinline__ int lds_off(int row, int c) { return row * kBK + swz(row, c) * 8; }
+// Swizzle for tiles written by LDS DMA (whole 8-row groups at once): rows r and r + 8 differ in
+// bit 0 of the pattern, which keeps 16-row fragment reads conflict-free for 32 or 64 banks, and the
+// pattern does not depend on which 16-row fragment is read (one base register, immediate offsets).
+__device__ __forceinline__ int swz_dma(int row, int c) { return c ^ ((row & 7) ^ ((row >> 3) & 1)); }
+__device__ __forceinline__ int lds_off_dma(int row, int c) { return row * kBK + swz_dma(row, c) * 8; }
 
 template <typename T>
 __device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c);
@@ -295,6 +300,171 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma(
 }
 
 // --------------------------------------------------------------------------------------------
+// The f16 / bf16 kernel for K-contiguous B ([N, K], nn.Linear weights) with K % 64 == 0.
+// Tiles move global -> LDS with gfx950's LDS DMA (global_load_lds_dwordx4): no staging registers
+// and no LDS store instructions. One DMA instruction writes 64 lanes x 16 bytes = 8 consecutive
+// tile rows; lane L fills physical chunk L % 8 of row L / 8, so it fetches the logical chunk that
+// the XOR swizzle maps there. Rows past M / N are clamped to the last row (their results are
+// never stored). Two LDS stages live in separate arrays and the k loop is unrolled by two, so the
+// stage being read and the stage being filled are distinct objects; tile k+2 streams in while
+// tile k+1 is multiplied. One barrier per k-tile.
+// --------------------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+
+#ifndef AK_GEMM_STEP_FENCE
+#define AK_GEMM_STEP_FENCE 1
+#endif
+constexpr bool kStepFence = AK_GEMM_STEP_FENCE != 0;
+
+// One LDS-DMA transfer: each lane moves 16 bytes from g to lds_row_base + lane * 16. Kept out of
+// the kernel's lambdas: the device-only builtin there makes the host pass drop the kernel stubs.
+__device__ __forceinline__ void dma16(const uint16_t* g, uint16_t* lds_row_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_row_base, 16, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(N | (0x7 << 4) | (0xf << 8));  // vmcnt(N), expcnt / lgkmcnt untouched
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI>
+__global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B0, const uint16_t* __restrict__ B1,
+    uint16_t* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
+    int tiles_m, int tiles_n) {
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int A_INS = BM / 8 / NW;  // DMA instructions per wave per tile for A
+  constexpr int B_INS = BN / 8 / NW;  // ... per B matrix
+  static_assert(A_INS * 8 * NW == BM && B_INS * 8 * NW == BN, "tile rows split over waves");
+  constexpr int INS = A_INS + NB * B_INS;
+  static_assert(INS < 16, "outstanding DMA per tile fits vmcnt");
+
+  __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * kBK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA1[BM * kBK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB0[NB][BN * kBK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB1[NB][BN * kBK];
+
+  int tm, tn;
+  tile_coords(tiles_m, tiles_n, &tm, &tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int lane = lane_id(), wid = wave_id();
+  const int wm = wid / WN, wn = wid % WN;
+  const int r_in = lane >> 3, pc = lane & 7;
+  const uint16_t* Bm[2] = {B0, B1};
+
+  // Per-lane element offsets (fixed over k; the host guarantees they fit 32 bits) of the row and
+  // chunk each DMA instruction fetches: physical chunk pc of a row holds logical chunk
+  // swz_dma(row, pc) (the XOR pattern is its own inverse).
+  int oa[A_INS];
+#pragma unroll
+  for (int i = 0; i < A_INS; ++i) {
+    const int row = (i * NW + wid) * 8 + r_in;
+    oa[i] = min(m0 + row, M - 1) * (int)lda + swz_dma(row, pc) * 8;
+  }
+  int ob[B_INS];
+#pragma unroll
+  for (int i = 0; i < B_INS; ++i) {
+    const int row = (i * NW + wid) * 8 + r_in;
+    ob[i] = min(n0 + row, N - 1) * (int)ldb + swz_dma(row, pc) * 8;
+  }
+
+  auto issue = [&](int k0, uint16_t* sa, uint16_t (*sb)[BN * kBK]) {
+#pragma unroll
+    for (int i = 0; i < A_INS; ++i)
+      dma16(A + (oa[i] + k0), sa + (i * NW + wid) * 8 * kBK);
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int i = 0; i < B_INS; ++i)
+        dma16(Bm[b] + (ob[i] + k0), sb[b] + (i * NW + wid) * 8 * kBK);
+  };
+
+  f32x4 acc[NB][FM][FN];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[b][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int fr = lane & 15, fc = lane >> 4;
+  auto compute = [&](const uint16_t* sa, const uint16_t (*sb)[BN * kBK]) {
+#pragma unroll
+    for (int s = 0; s < kBK / 32; ++s) {
+      u32x4 fa[FM], fb[NB][FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        fa[i] = *reinterpret_cast<const u32x4*>(&sa[lds_off_dma(wm * WTM + i * 16 + fr, s * 4 + fc)]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          fb[b][j] = *reinterpret_cast<const u32x4*>(&sb[b][lds_off_dma(wn * WTN + j * 16 + fr, s * 4 + fc)]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) acc[b][i][j] = mfma16x16x32<T>(fb[b][j], fa[i], acc[b][i][j]);
+      // Optionally keep the next k-step's fragment loads below these MFMAs.
+      if constexpr (kStepFence) __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  const int KT = K / kBK;
+  issue(0, sA0, sB0);
+  if (KT > 1) {
+    issue(kBK, sA1, sB1);
+    wait_vmcnt<INS>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    compute(sA0, sB0);  // tile kt (stage 0)
+    wait_vmcnt<0>();    // tile kt + 1 has landed in stage 1
+    __syncthreads();    // ... for every wave, and stage 0 is no longer read
+    if (kt + 2 < KT) issue((kt + 2) * kBK, sA0, sB0);
+    compute(sA1, sB1);  // tile kt + 1 (stage 1)
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (kt + 3 < KT) issue((kt + 3) * kBK, sA1, sB1);
+  }
+  if (kt < KT) compute(sA0, sB0);  // odd tile count: the last tile sits in stage 0
+
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = m0 + wm * WTM + i * 16 + fr;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * WTN + j * 16 + fc * 4;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (NB == 1) v[e] = acc[0][i][j][e];
+        else v[e] = gate_up<T, EPI>(acc[0][i][j][e], acc[1][i][j][e]);
+      }
+      uint16_t* cp = C + (int64_t)m * ldc + n;
+      if (n + 3 < N) {
+        u32x2 o;
+        o[0] = (uint32_t)T::from_f(v[0]) | ((uint32_t)T::from_f(v[1]) << 16);
+        o[1] = (uint32_t)T::from_f(v[2]) | ((uint32_t)T::from_f(v[3]) << 16);
+        *reinterpret_cast<u32x2*>(cp) = o;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) cp[e] = T::from_f(v[e]);
+      }
+    }
+  }
+}
+
+// --------------------------------------------------------------------------------------------
 // fp32 GEMM: v_mfma_f32_16x16x4_f32 keeps full fp32 products (no reduced-precision inputs).
 // Block 128x128x16, 4 waves of 64x64. A: [BM][BK+1] (padded), B: [BK][BN+16] for [K,N] input or
 // [BN][BK+1] for [N,K] input.
@@ -302,9 +472,9 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma(
 constexpr int kF32BM = 128, kF32BN = 128, kF32BK = 16;
 
 // s += v with the lost low-order bits kept in c (Kahan). No multiplies, so no contraction applies.
-__device__ __forceinline__ void kahan_add(float& s, float& c, float v) {
-  const float y = v - c;
-  const float t = s + y;
+__device__ __forceinline__ void kahan_add(f32x4& s, f32x4& c, const f32x4& v) {
+  const f32x4 y = v - c;
+  const f32x4 t = s + y;
   c = (t - s) - y;
   s = t;
 }
@@ -394,9 +564,7 @@ __global__ __launch_bounds__(256) void gemm_f32(const float* __restrict__ A, con
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) kahan_add(acc[i][j][e], comp[i][j][e], part[i][j][e]);
+      for (int j = 0; j < 4; ++j) kahan_add(acc[i][j], comp[i][j], part[i][j]);
     if (kt + 1 < KT) sstore(cur ^ 1);
     __syncthreads();
   }
@@ -482,6 +650,35 @@ static void launch_gemm_tiled(const void* A, const void* B0, const void* B1, voi
   }
 }
 
+#ifndef AK_GEMM_DMA
+#define AK_GEMM_DMA 1
+#endif
+constexpr bool kUseDma = AK_GEMM_DMA != 0;
+
+template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI>
+static void launch_dma_cfg(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
+                           int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
+  const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(N, BN);
+  gemm_dma<T, BM, BN, WM, WN, NB, EPI><<<tiles_m * tiles_n, WM * WN * kWave, 0, s>>>(
+      (const uint16_t*)A, (const uint16_t*)B0, (const uint16_t*)B1, (uint16_t*)C, M, N, K, lda, ldb, ldc,
+      tiles_m, tiles_n);
+}
+
+template <typename T, int NB, int EPI>
+static void launch_gemm_dma(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
+                            int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
+  const TileCfg t = pick_tile(M, N, NB);
+  if constexpr (NB == 1) {
+    if (t.bm == 256 && t.bn == 256) launch_dma_cfg<T, 256, 256, 2, 4, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+    else if (t.bm == 256) launch_dma_cfg<T, 256, 128, 4, 2, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+    else launch_dma_cfg<T, 128, 128, 2, 2, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+  } else {
+    if (t.bm == 256 && t.bn == 256) launch_dma_cfg<T, 256, 128, 2, 4, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+    else if (t.bm == 256) launch_dma_cfg<T, 256, 64, 4, 2, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+    else launch_dma_cfg<T, 128, 64, 2, 2, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+  }
+}
+
 template <typename T, int NB, int EPI>
 static int launch_gemm16(const void* A, const void* B0, const void* B1, void* C, int64_t M,
                          int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, bool bt,
@@ -490,6 +687,12 @@ static int launch_gemm16(const void* A, const void* B0, const void* B1, void* C,
              host_aligned16(B0) && (!B1 || host_aligned16(B1)) && (((uintptr_t)C) & 7u) == 0;
   if (!bt) vec = vec && N % 8 == 0;
   const int m = (int)M, n = (int)N, k = (int)K;
+  // LDS-DMA path: nn.Linear-layout B, K a multiple of 64, 32-bit element offsets
+  const bool fits32 = M * lda < INT_MAX && N * ldb < INT_MAX;
+  if (bt && vec && K % kBK == 0 && K > 0 && fits32 && kUseDma) {
+    launch_gemm_dma<T, NB, EPI>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s);
+    return record_launch();
+  }
   if (bt) {
     if (vec) launch_gemm_tiled<T, true, true, NB, EPI>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s);
     else launch_gemm_tiled<T, true, false, NB, EPI>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s);
@@ -575,12 +778,10 @@ __global__ __launch_bounds__(256) void gate_up_f32(const float* __restrict__ X, 
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          kahan_add(ag[i][j][e], cg[i][j][e], pg[i][j][e]);
-          kahan_add(au[i][j][e], cu[i][j][e], pu[i][j][e]);
-        }
+      for (int j = 0; j < 2; ++j) {
+        kahan_add(ag[i][j], cg[i][j], pg[i][j]);
+        kahan_add(au[i][j], cu[i][j], pu[i][j]);
+      }
     __syncthreads();
   }
 #pragma unroll

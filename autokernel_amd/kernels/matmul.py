@@ -26,6 +26,24 @@ def _b_layout(B: torch.Tensor) -> tuple[torch.Tensor, int, int]:
     return Bc, max(N, 1), 0
 
 
+# [K, N] operands at least this large are transposed once (ak_transpose) and multiplied by the
+# K-contiguous LDS-DMA GEMM; the transpose moves 2*K*N elements, far less than the register
+# transpose inside the [K, N] GEMM kernel costs at these sizes.
+NN_TRANSPOSE_MIN_MNK = 256 * 256 * 256
+
+
+def transpose(B: torch.Tensor) -> torch.Tensor:
+    """Contiguous B.T of a row-major 2-D tensor via ak_transpose."""
+    K, N = B.shape
+    out = torch.empty((N, K), device=B.device, dtype=B.dtype)
+    code = _lib.dtype_code(B, "transpose")
+    with device_guard(B):
+        st = _lib.load().ak_transpose(code, B.data_ptr(), out.data_ptr(), K, N, B.stride(0), max(K, 1),
+                                      _lib.stream_of(B))
+    _lib.check(st, "ak_transpose", shape=tuple(B.shape), dtype=B.dtype)
+    return out
+
+
 def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """C = A @ B for 2-D A [M, K] and 2-D B [K, N] (B may be a transposed [N, K] view)."""
     M, K = A.shape
@@ -39,6 +57,9 @@ def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> t
         A = A.contiguous()
     lda = A.stride(0) if M > 1 else max(K, 1)
     Bt, ldb, bt = _b_layout(B)
+    if (bt == 0 and A.dtype != torch.float32 and K % 64 == 0 and K % 8 == 0 and
+            M * N * K >= NN_TRANSPOSE_MIN_MNK):
+        Bt, ldb, bt = transpose(Bt if Bt.stride(0) == ldb and Bt.stride(1) == 1 else Bt.contiguous()), K, 1
     C = out if out is not None else torch.empty((M, N), device=A.device, dtype=A.dtype)
     if K == 0:
         return C.zero_()

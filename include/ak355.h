@@ -131,6 +131,14 @@ int ak_gemm(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t
             int64_t lda, int64_t ldb, int64_t ldc, int b_trans, hipStream_t stream);
 
 /*
+ * 2-D transpose: dst[c][r] = src[r][c] for a rows x cols matrix with row strides ld_src / ld_dst.
+ * No counterpart in the reference: the layout helper the matmul drop-in uses to feed a [K, N] B
+ * operand to the K-contiguous GEMM path (one extra read and write of B).
+ */
+int ak_transpose(int dtype, const void* src, void* dst, int64_t rows, int64_t cols,
+                 int64_t ld_src, int64_t ld_dst, hipStream_t stream);
+
+/*
  * Fused gate/up projection of the SwiGLU MLP:
  *   h = round(act(round(x @ w_gate.T))) * round(x @ w_up.T), rounded to the element type.
  * x: [M, D]; w_gate, w_up: [H, D] (nn.Linear layout); h: [M, H].

@@ -294,3 +294,15 @@ def test_fused_mlp_activations_f16(gpu):
     for act in ("silu", "gelu", "relu2", "none"):
         out = kernels.get("fused_mlp")(x.to(gpu), wg.to(gpu), wu.to(gpu), wd.to(gpu), act)
         assert_close(out, R.fused_mlp_ref(x, wg, wu, wd, act), 1e-2, 1e-2, f"mlp {act}")
+
+
+def test_transpose_layout_helper(gpu):
+    from autokernel_amd.kernels.matmul import transpose
+    g = torch.Generator().manual_seed(11)
+    for (r, c) in ((64, 64), (4096, 4096), (1023, 1537), (7, 300), (300, 7)):
+        for dt in (torch.float16, torch.bfloat16, torch.float32):
+            x = torch.randn(r, c, generator=g).to(dt)
+            assert torch.equal(transpose(x.to(gpu)).cpu(), x.t().contiguous()), (r, c, dt)
+    big = torch.randn(128, 200, generator=g).half()
+    view = big.to(gpu)[:, 8:136]  # row stride 200
+    assert torch.equal(transpose(view).cpu(), big[:, 8:136].t().contiguous())
