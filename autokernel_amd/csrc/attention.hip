@@ -13,11 +13,12 @@
 //     is a fixed permutation of the keys; V^T is stored in LDS with the same permutation, so
 //     the contraction is unchanged. O^T also has the query as its column, so the online-softmax
 //     rescale is lane-local.
-//   * V is transposed on its way into LDS (4 keys x 8 dims per thread through v_perm_b32);
-//     K stays [key][d]. Both use an XOR chunk swizzle that keeps fragment reads and the
-//     transposed writes free of bank conflicts.
+//   * V is transposed on its way into LDS (4 keys x 8 dims per thread through v_perm_b32; the 8
+//     lanes of a write phase cover 8 key-quads of one V^T row); K stays [key][d]. Both use the
+//     XOR chunk swizzle c ^ (row & 7), under which fragment reads and these writes are
+//     conflict-free.
 //   * Causal: key tiles past a block's last query are never loaded, tiles past a wave's last
-//     query are skipped by that wave, and blocks are issued heaviest-first.
+//     query are skipped by that wave, and blocks are issued heaviest-first over all heads.
 //   * f16 inputs: the reference rounds Q K^T to f16 and scales in f16, so scores beyond the f16
 //     range become +-inf (and produce its NaN rows). Per tile, a wave-wide test of the largest
 //     |score| enables an exact per-element emulation only when such a score exists.
@@ -27,12 +28,23 @@
 
 namespace ak {
 
-constexpr int kFaBQ = 128;   // query rows per block
 constexpr int kFaBKV = 64;   // keys per tile
-constexpr int kFaThreads = 256;
+// Lazy rescale: the running max used as the exp2 base is only raised when a tile's max exceeds
+// it by more than this (log2 units), so P stays <= 2^8 (exact in f16 / bf16 range) and the O
+// accumulator is rescaled only a handful of times per row instead of on most tiles.
+constexpr float kFaRescaleSlack = 8.0f;
+
+#ifndef AK_FA_WAVES
+#define AK_FA_WAVES 4
+#endif
+constexpr int kFaWaves = AK_FA_WAVES;        // waves per block, 32 query rows each
+constexpr int kFaBQ = 32 * kFaWaves;         // query rows per block
+constexpr int kFaThreads = kFaWaves * 64;
 constexpr float kFaLog2e = 1.4426950408889634f;
 
-__device__ __forceinline__ int fa_swz(int row, int c) { return c ^ ((row ^ (row >> 3)) & 7); }
+// 16-byte chunk c of an LDS row is stored at chunk c ^ (row & 7): a ds_read_b128 phase of 8 lanes
+// reading 8 consecutive rows at one logical chunk hits 8 different slots.
+__device__ __forceinline__ int fa_swz(int row, int c) { return c ^ (row & 7); }
 
 // Physical position of key offset o (0..15) inside its 16-key group in V^T: the MFMA's logical
 // k index h*8 + e (lane half h, element e) carries key 4h + (e & 3) + 8 * (e >> 2).
@@ -50,11 +62,11 @@ __device__ __forceinline__ f32x16 mfma32x32x16<TBF16>(const u32x4& a, const u32x
 }
 
 template <typename T, int D>
-__global__ __launch_bounds__(kFaThreads, 2) void fa_fwd(
+__global__ __launch_bounds__(kFaThreads, 8 / kFaWaves) void fa_fwd(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, int Hq, int group, int Sq, int Sk, int64_t qsb, int64_t qsh,
     int64_t qss, int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss,
-    int64_t osb, int64_t osh, int64_t oss, int causal, float scale_log2, float ovf_thresh) {
+    int64_t osb, int64_t osh, int64_t oss, int causal, float scale_log2, float ovf_thresh, int nbh) {
   constexpr int DC = D / 8;              // 16-byte chunks per K row
   constexpr int NDB = D / 32;            // 32-wide d blocks of O^T
   constexpr int NS = D / 16;             // 16-deep d steps of S^T
@@ -66,9 +78,13 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fwd(
   __shared__ __attribute__((aligned(16))) uint16_t sK[2][kFaBKV * D];
   __shared__ __attribute__((aligned(16))) uint16_t sV[2][D * kFaBKV];
 
-  const int nqb = gridDim.x;
-  const int qb = causal ? (nqb - 1 - (int)blockIdx.x) : (int)blockIdx.x;  // heaviest first
-  const int h = blockIdx.y, b = blockIdx.z;
+  // 1-D grid ordered by q-block, heaviest first across all (batch, head): blocks are dispatched in
+  // index order, so under a causal mask the long blocks start first and short ones fill the tail.
+  const int bh = (int)(blockIdx.x % (unsigned)nbh);
+  const int qi = (int)(blockIdx.x / (unsigned)nbh);
+  const int nqb = (Sq + kFaBQ - 1) / kFaBQ;
+  const int qb = causal ? (nqb - 1 - qi) : qi;
+  const int h = bh % Hq, b = bh / Hq;
   const int hk = h / group;
   const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
   const int l32 = lane & 31, hh = lane >> 5;
@@ -105,7 +121,7 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fwd(
 #pragma unroll
     for (int i = 0; i < V_U; ++i) {
       const int u = tid + i * kFaThreads;
-      const int dg = u % (D / 8), kq = u / (D / 8);
+      const int kq = u % (kFaBKV / 4), dg = u / (kFaBKV / 4);
       if (u < V_UNITS) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -127,7 +143,7 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fwd(
 #pragma unroll
     for (int i = 0; i < V_U; ++i) {
       const int u = tid + i * kFaThreads;
-      const int dg = u % (D / 8), kq = u / (D / 8);
+      const int kq = u % (kFaBKV / 4), dg = u / (kFaBKV / 4);
       if (u >= V_UNITS) continue;
       const int pos = (kq >> 2) * 16 + fa_kperm((kq & 3) * 4);  // physical key position
       const int c = pos >> 3, off = pos & 7;
@@ -216,9 +232,13 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fwd(
 #pragma unroll
         for (int v = 0; v < 16; ++v) mt = fmaxf(mt, s[kb][v]);
       mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-      const float m_new = fmaxf(m_run, fused ? mt * scale_log2 : mt);
+      const float m_tile = fused ? mt * scale_log2 : mt;
+      // raise the base only when the tile's max passes it by more than the slack (or it is
+      // still -inf / the tile holds +inf / NaN, which must propagate exactly)
+      const float m_new = (m_tile > m_run + kFaRescaleSlack || m_run == -INFINITY || !(m_tile == m_tile) ||
+                           m_tile == INFINITY) ? fmaxf(m_run, m_tile) : m_run;
       const float base = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - base);
+      const float alpha = (m_new == m_run) ? 1.0f : __builtin_amdgcn_exp2f(m_run - base);
       const float mul = fused ? scale_log2 : 1.0f;
       float ps = 0.f;
       u32x4 pf[4];
@@ -285,13 +305,15 @@ template <typename T, int D>
 static int launch_fa(const void* Q, const void* K, const void* V, void* O, int64_t B, int64_t Hq,
                      int64_t Hkv, int64_t Sq, int64_t Sk, const int64_t* qs, const int64_t* ks,
                      const int64_t* vs, const int64_t* os, int causal, float sm_scale, hipStream_t st) {
-  const dim3 grid((unsigned)cdiv(Sq, kFaBQ), (unsigned)Hq, (unsigned)B);
+  const int64_t nblocks = cdiv(Sq, kFaBQ) * Hq * B;
+  if (nblocks > INT_MAX) return AK_EINVAL;
+  const dim3 grid((unsigned)nblocks);
   // Scores whose f16 rounding (or f16 scaling by sm_scale) overflows become +-inf.
   const float thr = 65520.0f / fmaxf(1.0f, fabsf(sm_scale));
   fa_fwd<T, D><<<grid, kFaThreads, 0, st>>>(
       (const uint16_t*)Q, (const uint16_t*)K, (const uint16_t*)V, (uint16_t*)O, (int)Hq,
       (int)(Hq / Hkv), (int)Sq, (int)Sk, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1],
-      vs[2], os[0], os[1], os[2], causal, sm_scale * kFaLog2e, thr);
+      vs[2], os[0], os[1], os[2], causal, sm_scale * kFaLog2e, thr, (int)(Hq * B));
   return record_launch();
 }
 
@@ -309,7 +331,7 @@ extern "C" int ak_flash_attn_fwd(int dtype, const void* Q, const void* K, const 
   if (!q_strides || !k_strides || !v_strides || !o_strides) return AK_EINVAL;
   if (B == 0 || Hq == 0 || Sq == 0) return AK_OK;
   if (!Q || !K || !V || !O) return AK_EINVAL;
-  if (B > 65535 || Hq > 65535 || Sq > INT_MAX || Sk > INT_MAX) return AK_EINVAL;
+  if (B * Hq > INT_MAX || Sq > INT_MAX || Sk > INT_MAX) return AK_EINVAL;
   if (dtype != AK_F16 && dtype != AK_BF16) return AK_EUNSUPPORTED;
   if (D != 64 && D != 128) return AK_EUNSUPPORTED;
   // 16-byte aligned rows: every stride a multiple of 8 elements, 16-byte aligned bases

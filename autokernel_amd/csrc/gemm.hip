@@ -30,10 +30,19 @@ constexpr int kKC = kBK / 8;      // 16-byte chunks per tile row
 __device__ __forceinline__ int swz(int row, int c) { return c ^ ((row ^ (row >> 3)) & 7); }
 // element offset of chunk c of row `row` in a [rows][64] tile
 __device__ __forceinline__ int lds_off(int row, int c) { return row * kBK + swz(row, c) * 8; }
-// Swizzle for tiles written by LDS DMA (whole 8-row groups at once): rows r and r + 8 differ in
-// bit 0 of the pattern, which keeps 16-row fragment reads conflict-free for 32 or 64 banks, and the
-// pattern does not depend on which 16-row fragment is read (one base register, immediate offsets).
-__device__ __forceinline__ int swz_dma(int row, int c) { return c ^ ((row & 7) ^ ((row >> 3) & 1)); }
+// Swizzle for tiles written by LDS DMA (whole 8-row groups at once). gfx950 serves a 64-lane
+// ds_read_b128 in 8-lane phases of 128 bytes, so chunk c ^ (row & 7) makes the 8 rows of a phase
+// hit 8 different 16-byte slots (measured: SQ_LDS_BANK_CONFLICT 0 vs 50% for a variant with an
+// extra row-bit-3 term, 75% unswizzled). The pattern does not depend on which 16-row fragment is
+// read, so fragment addresses are one base register plus immediate offsets.
+#ifndef AK_GEMM_DMA_SWZ
+#define AK_GEMM_DMA_SWZ 2
+#endif
+__device__ __forceinline__ int swz_dma(int row, int c) {
+  if constexpr (AK_GEMM_DMA_SWZ == 1) return c ^ ((row & 7) ^ ((row >> 3) & 1));
+  else if constexpr (AK_GEMM_DMA_SWZ == 2) return c ^ (row & 7);
+  else return c;
+}
 __device__ __forceinline__ int lds_off_dma(int row, int c) { return row * kBK + swz_dma(row, c) * 8; }
 
 template <typename T>

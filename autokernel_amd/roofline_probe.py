@@ -1,4 +1,15 @@
-"""HBM traffic evidence for the bandwidth-bound kernels (run under rocprofv3 --pmc).
+"""Counter evidence for the roofline claims (run under rocprofv3 --pmc).
+
+HBM traffic of the bandwidth-bound kernels (`run` / `summarize`) and MFMA / LDS activity of the
+matrix kernels (`run_mfma` / `summarize_mfma`):
+
+    rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE GRBM_GUI_ACTIVE \
+        -d DIR -o mfma_a --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma
+    rocprofv3 --pmc SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_WAIT_INST_LDS SQ_INSTS_MFMA SQ_INSTS_VALU SQ_INSTS_LDS SQ_WAVE_CYCLES \
+        -d DIR -o mfma_b --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma
+    python -m autokernel_amd.roofline_probe summarize_mfma DIR
+
+HBM traffic of the bandwidth-bound kernels:
 
     rocprofv3 --pmc FETCH_SIZE -d DIR -o fetch --output-format csv -- python -m autokernel_amd.roofline_probe run
     rocprofv3 --pmc WRITE_SIZE -d DIR -o write --output-format csv -- python -m autokernel_amd.roofline_probe run
@@ -63,6 +74,64 @@ def run() -> None:
     print("roofline_probe: done", flush=True)
 
 
+MFMA_PROBES = [  # kernel-name fragment, label, flops per launch
+    ("gemm_dma<ak::TBF16, 256, 256", "matmul bf16 4096^3 (NT, LDS-DMA)", 2 * 4096 ** 3),
+    ("gemm_dma<ak::TBF16, 256, 128, 2, 4, 2", "fused_mlp gate/up bf16 2048x4096 H=11008", 2 * 2048 * 4096 * 11008 * 2),
+    ("fa_fwd<ak::TF16, 128>", "flash_attention f16 causal [4,32,2048,128]", 2 * 2 * 4 * 32 * 128 * (2048 * 2049 // 2)),
+]
+
+
+def run_mfma() -> None:
+    import torch
+
+    from . import kernels, spec
+    dev = torch.device("cuda:0")
+    flush = torch.empty(512 * 2 ** 20, dtype=torch.uint8, device=dev)
+    m = spec.baseline_matmul(device=dev)
+    Bt = m["B"].t().contiguous()
+    f = spec.baseline_fused_mlp(device=dev)
+    a = spec.baseline_attention(device=dev)
+    calls = [lambda: kernels.get("matmul")(m["A"], Bt.t()), lambda: kernels.get("fused_mlp")(**f),
+             lambda: kernels.get("flash_attention")(**a)]
+    for c in calls:
+        for _ in range(3):
+            flush.zero_()
+            c()
+    torch.cuda.synchronize()
+    print("roofline_probe: done", flush=True)
+
+
+def summarize_mfma(dirpath: str) -> None:
+    data = _read(dirpath)
+    lines = ["# MFMA and LDS activity of the matrix kernels (rocprofv3 PMC)", "",
+             "Commands (two counter passes, then the summary):", "",
+             "    rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE GRBM_GUI_ACTIVE -d DIR -o mfma_a --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma",
+             "    rocprofv3 --pmc SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_WAIT_INST_LDS SQ_INSTS_MFMA SQ_INSTS_VALU SQ_INSTS_LDS SQ_WAVE_CYCLES -d DIR -o mfma_b --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma",
+             "    python -m autokernel_amd.roofline_probe summarize_mfma DIR", "",
+             "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 256 CUs x 4 SIMDs); LDS bank-conflict",
+             "rate = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE (the rocprof-compute definitions). Averages per dispatch.", "",
+             "| kernel | workload | MFMA busy | LDS bank-conflict rate | VALU active / wave-cycle | LDS active / wave-cycle | LDS wait / wave-cycle |",
+             "|---|---|---|---|---|---|---|"]
+
+    def avg(d, k):
+        v = d.get(k, [])
+        return sum(v) / len(v) if v else float("nan")
+
+    for frag, label, flops in MFMA_PROBES:
+        rows = [(k, v) for k, v in data.items() if frag in k]
+        if not rows:
+            continue
+        name, d = rows[0]
+        # GRBM_GUI_ACTIVE is summed over the 8 XCDs; MFMA busy cycles are counted per SIMD
+        busy = avg(d, "SQ_VALU_MFMA_BUSY_CYCLES") / (avg(d, "GRBM_GUI_ACTIVE") / 8 * 256 * 4)
+        conf = avg(d, "SQ_LDS_BANK_CONFLICT") / max(avg(d, "SQ_LDS_IDX_ACTIVE"), 1)
+        wc = max(avg(d, "SQ_WAVE_CYCLES"), 1)
+        lines.append(f"| {name.split('(')[0]} | {label} | {100 * busy:.1f}% | {100 * conf:.1f}% | "
+                     f"{avg(d, 'SQ_ACTIVE_INST_VALU') / wc:.3f} | {avg(d, 'SQ_ACTIVE_INST_LDS') / wc:.3f} | "
+                     f"{avg(d, 'SQ_WAIT_INST_LDS') / wc:.3f} |")
+    print("\n".join(lines))
+
+
 def _read(dirpath: str):
     """{kernel name: {counter: [values per dispatch]}} from rocprofv3 counter_collection CSVs."""
     out = defaultdict(lambda: defaultdict(list))
@@ -109,7 +178,12 @@ def summarize(dirpath: str) -> None:
 
 
 if __name__ == "__main__":
-    if len(sys.argv) > 1 and sys.argv[1] == "summarize":
+    cmd = sys.argv[1] if len(sys.argv) > 1 else "run"
+    if cmd == "summarize":
         summarize(sys.argv[2])
+    elif cmd == "summarize_mfma":
+        summarize_mfma(sys.argv[2])
+    elif cmd == "run_mfma":
+        run_mfma()
     else:
         run()
