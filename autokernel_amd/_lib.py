@@ -34,7 +34,8 @@ SIGNATURES: dict[str, list] = {
     "ak_layernorm": [_i, _p, _p, _p, _p, _i64, _i64, _f, _p],
     "ak_softmax": [_i, _p, _p, _i64, _i64, _p],
     "ak_rope": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
-    "ak_rope_f32_tables": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
+    "ak_rope_f32_tables": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
+    "ak_rmsnorm_rsqrt": [_i, _p, _p, _p, _i64, _i64, _f, _p],
     "ak_cross_entropy": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "ak_reduce_sum": [_i, _p, _p, _i64, _i64, _i64, _p],
     "ak_reduce_max": [_i, _p, _p, _i64, _i64, _i64, _p],

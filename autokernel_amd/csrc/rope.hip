@@ -5,8 +5,9 @@
 //   y[2i+1] = rnd(rnd(x[2i]*sin[i]) + rnd(x[2i+1]*cos[i]))
 // rnd() rounds to the element type, as each elementwise tensor op of the reference does; for
 // fp32 no fused multiply-add is formed, so every element is bit-identical to the tensor ops.
-// The fast path moves one 16-byte vector of x (4 pairs for f16 / bf16) and two 8-byte table
-// slices per thread; the table rows stay hot in L2 across heads.
+// The fast path moves 16-byte vectors of x (4 pairs for f16 / bf16) with two 8-byte table slices
+// each, four vectors per thread with all loads issued first; table rows stay hot in L2 across
+// heads.
 #include <limits.h>
 
 #include "ak_common.h"
@@ -20,23 +21,13 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
   *y2 = T::rnd(T::rnd(x1 * s) + T::rnd(x2 * c));
 }
 
+// Each thread rotates kCpt 16-byte chunks spaced one grid apart, issuing all loads before any
+// arithmetic so a wave keeps kCpt x 1 KB of x in flight.
+constexpr int kRopeCpt = 4;
+
 template <typename T>
-__global__ __launch_bounds__(256) void rope_vec(const typename T::S* __restrict__ x,
-                                                const typename T::S* __restrict__ ct,
-                                                const typename T::S* __restrict__ st,
-                                                typename T::S* __restrict__ y, int64_t nchunks,
-                                                int chunks_per_row, int half, int64_t table_rows,
-                                                int64_t rep_inner) {
-  using S = typename T::S;
+__device__ __forceinline__ u32x4 rope_chunk(const u32x4& xv, const typename T::S* cp, const typename T::S* sp) {
   constexpr int kP = T::kVec / 2;  // pairs per 16-byte vector
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= nchunks) return;
-  const int64_t row = i / chunks_per_row;
-  const int c = (int)(i - row * chunks_per_row);
-  const int64_t trow = (row / rep_inner) % table_rows;
-  const u32x4 xv = ld16(x + i * T::kVec);
-  const S* cp = ct + trow * half + c * kP;
-  const S* sp = st + trow * half + c * kP;
   float cf[kP], sf[kP];
   if constexpr (kP == 4) {  // 2-byte types: 8 bytes of cos, 8 bytes of sin
     const u32x2 cv = *reinterpret_cast<const u32x2*>(cp);
@@ -62,7 +53,35 @@ __global__ __launch_bounds__(256) void rope_vec(const typename T::S* __restrict_
     T::set_elem(yv, 2 * p, y1);
     T::set_elem(yv, 2 * p + 1, y2);
   }
-  st16(y + i * T::kVec, yv);
+  return yv;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rope_vec(const typename T::S* __restrict__ x,
+                                                const typename T::S* __restrict__ ct,
+                                                const typename T::S* __restrict__ st,
+                                                typename T::S* __restrict__ y, int64_t nchunks,
+                                                int chunks_per_row, int half, int64_t table_rows,
+                                                int64_t rep_inner) {
+  constexpr int kP = T::kVec / 2;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  u32x4 xv[kRopeCpt];
+#pragma unroll
+  for (int u = 0; u < kRopeCpt; ++u) {
+    const int64_t i = i0 + u * stride;
+    if (i < nchunks) xv[u] = ld16(x + i * T::kVec);
+  }
+#pragma unroll
+  for (int u = 0; u < kRopeCpt; ++u) {
+    const int64_t i = i0 + u * stride;
+    if (i < nchunks) {
+      const int64_t row = i / chunks_per_row;
+      const int c = (int)(i - row * chunks_per_row);
+      const int64_t trow = (row / rep_inner) % table_rows;
+      st16(y + i * T::kVec, rope_chunk<T>(xv[u], ct + trow * half + c * kP, st + trow * half + c * kP));
+    }
+  }
 }
 
 // Any alignment: one pair per thread.
@@ -85,20 +104,25 @@ __global__ __launch_bounds__(256) void rope_scalar(const typename T::S* __restri
 }
 // Model form (the reference's LLaMA apply_rotary_emb, models/llama_7b.py:40-48): x upcast to
 // fp32, rotated by fp32 cos / sin as a complex multiply, rounded once to x's dtype.
+// x rows are grouped rep_inner (heads) to a token, token t starting at element t * x_tok_stride
+// (dense when x_tok_stride = rep_inner * head_dim; larger when q / k are column slices of a fused
+// QKV projection); y is dense.
 template <typename T>
 __global__ __launch_bounds__(256) void rope_f32t_vec(const typename T::S* __restrict__ x,
                                                     const float* __restrict__ ct,
                                                     const float* __restrict__ st,
                                                     typename T::S* __restrict__ y, int64_t nchunks,
                                                     int chunks_per_row, int half, int64_t table_rows,
-                                                    int64_t rep_inner) {
+                                                    int64_t rep_inner, int64_t x_tok_stride) {
   constexpr int kP = T::kVec / 2;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= nchunks) return;
   const int64_t row = i / chunks_per_row;
   const int c = (int)(i - row * chunks_per_row);
-  const int64_t trow = (row / rep_inner) % table_rows;
-  const u32x4 xv = ld16(x + i * T::kVec);
+  const int64_t tok = row / rep_inner;
+  const int64_t trow = tok % table_rows;
+  const int64_t xoff = tok * x_tok_stride + (row - tok * rep_inner) * (2 * half) + (int64_t)c * T::kVec;
+  const u32x4 xv = ld16(x + xoff);
   const float* cp = ct + trow * half + c * kP;
   const float* sp = st + trow * half + c * kP;
   u32x4 yv;
@@ -123,8 +147,8 @@ static int launch_rope(const void* x, const void* c, const void* s, void* y, int
   if (vec) {
     const int cpr = (int)(d / T::kVec);
     const int64_t n = rows * cpr;
-    rope_vec<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>((const S*)x, (const S*)c, (const S*)s,
-                                                            (S*)y, n, cpr, half, table_rows, rep_inner);
+    rope_vec<T><<<(unsigned)cdiv(n, 256 * kRopeCpt), 256, 0, stream>>>(
+        (const S*)x, (const S*)c, (const S*)s, (S*)y, n, cpr, half, table_rows, rep_inner);
   } else {
     const int64_t n = rows * half;
     rope_scalar<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>((const S*)x, (const S*)c, (const S*)s,
@@ -135,12 +159,14 @@ static int launch_rope(const void* x, const void* c, const void* s, void* y, int
 
 template <typename T>
 static int launch_rope_f32t(const void* x, const float* c, const float* s, void* y, int64_t rows,
-                            int64_t d, int64_t table_rows, int64_t rep_inner, hipStream_t stream) {
+                            int64_t d, int64_t table_rows, int64_t rep_inner, int64_t x_tok_stride,
+                            hipStream_t stream) {
   using S = typename T::S;
   const int cpr = (int)(d / T::kVec);
   const int64_t n = rows * cpr;
   rope_f32t_vec<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>((const S*)x, c, s, (S*)y, n, cpr,
-                                                                 (int)(d / 2), table_rows, rep_inner);
+                                                                 (int)(d / 2), table_rows, rep_inner,
+                                                                 x_tok_stride);
   return record_launch();
 }
 
@@ -160,13 +186,15 @@ extern "C" int ak_rope(int dtype, const void* x, const void* cos_t, const void* 
 
 extern "C" int ak_rope_f32_tables(int dtype, const void* x, const float* cos_t, const float* sin_t,
                                   void* y, int64_t rows, int64_t head_dim, int64_t table_rows,
-                                  int64_t rep_inner, hipStream_t stream) {
+                                  int64_t rep_inner, int64_t x_tok_stride, hipStream_t stream) {
   if (rows < 0 || head_dim < 0 || head_dim % 2 != 0 || head_dim > INT_MAX) return AK_EINVAL;
   if (rows == 0 || head_dim == 0) return AK_OK;
-  if (!x || !cos_t || !sin_t || !y || table_rows <= 0 || rep_inner <= 0) return AK_EINVAL;
+  if (!x || !cos_t || !sin_t || !y || table_rows <= 0 || rep_inner <= 0 || rows % rep_inner != 0) return AK_EINVAL;
+  if (x_tok_stride < rep_inner * head_dim) return AK_EINVAL;
   if (dtype != AK_F16 && dtype != AK_BF16) return AK_EUNSUPPORTED;
-  if (head_dim % 8 != 0 || !host_aligned16(x) || !host_aligned16(y)) return AK_EUNSUPPORTED;
+  if (head_dim % 8 != 0 || x_tok_stride % 8 != 0 || !host_aligned16(x) || !host_aligned16(y)) return AK_EUNSUPPORTED;
   if (rows * head_dim / 8 > (int64_t)UINT_MAX * 256) return AK_EINVAL;
-  if (dtype == AK_F16) return launch_rope_f32t<TF16>(x, cos_t, sin_t, y, rows, head_dim, table_rows, rep_inner, stream);
-  return launch_rope_f32t<TBF16>(x, cos_t, sin_t, y, rows, head_dim, table_rows, rep_inner, stream);
+  if (dtype == AK_F16)
+    return launch_rope_f32t<TF16>(x, cos_t, sin_t, y, rows, head_dim, table_rows, rep_inner, x_tok_stride, stream);
+  return launch_rope_f32t<TBF16>(x, cos_t, sin_t, y, rows, head_dim, table_rows, rep_inner, x_tok_stride, stream);
 }

@@ -13,6 +13,12 @@
 
 namespace ak {
 
+// Rows are touched once: nontemporal loads / stores keep them from displacing reused data.
+#ifndef AK_ROW_STREAM
+#define AK_ROW_STREAM 0
+#endif
+constexpr bool kRowStream = AK_ROW_STREAM != 0;
+
 // Butterfly over the L lanes of a segment (L <= 64): every lane ends with the segment result.
 template <int L>
 __device__ __forceinline__ float seg_sum(float v) {
@@ -89,7 +95,7 @@ struct RowRegs {
     for (int j = 0; j < VPT; ++j) {
       const int idx = gl + j * L;
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (idx < nvec) v = ld16(row + (int64_t)idx * T::kVec);
+      if (idx < nvec) v = kRowStream ? ld16_stream(row + (int64_t)idx * T::kVec) : ld16(row + (int64_t)idx * T::kVec);
 #pragma unroll
       for (int e = 0; e < T::kVec; ++e) f[j * T::kVec + e] = T::lane_elem(v, e);
     }
@@ -105,7 +111,8 @@ struct RowRegs {
         u32x4 v;
 #pragma unroll
         for (int e = 0; e < T::kVec; ++e) T::set_elem(v, e, f[j * T::kVec + e]);
-        st16(row + (int64_t)idx * T::kVec, v);
+        if constexpr (kRowStream) st16_stream(row + (int64_t)idx * T::kVec, v);
+        else st16(row + (int64_t)idx * T::kVec, v);
       }
     }
   }

@@ -23,16 +23,21 @@ __device__ __forceinline__ float block_reduce(float v, float* red) {
 //   sq = x**2; ms = mean(sq); t = ms + eps; rms = sqrt(t); q = x / rms; y = q * weight
 // so x*x rounds (and may overflow to inf) in f16 before the fp32-accumulated mean.
 // =============================================================================================
-template <typename T>
+// FORM 0: reference.py:28-29, y = (x / sqrt(mean(x^2) + eps)) * w.
+// FORM 1: a LLaMA block's module (models/llama_7b.py:28-30), y = x * rsqrt(mean(x^2) + eps) * w,
+// where rsqrt's result is itself a tensor rounded to the element type.
+template <typename T, int FORM>
 struct RmsStats {
-  __device__ __forceinline__ static float inv_rms(float ss, int cols, float eps) {
+  // the factor each x is multiplied by before its rounding
+  __device__ __forceinline__ static float scale(float ss, int cols, float eps) {
     const float ms = T::rnd(ss / (float)cols);
-    const float rms = T::rnd(sqrtf(T::rnd(ms + eps)));
-    return 1.0f / rms;  // x / rms == x * (1 / rms) to within one fp32 ulp before rounding
+    const float t = T::rnd(ms + eps);
+    if constexpr (FORM == 0) return 1.0f / T::rnd(sqrtf(t));  // x / rms to within one fp32 ulp
+    else return T::rnd(1.0f / sqrtf(t));
   }
 };
 
-template <typename T, int L, int VPT>
+template <typename T, int L, int VPT, int FORM>
 __global__ __launch_bounds__(RowGeom<L>::kThreads) void rmsnorm_rows(
     const typename T::S* __restrict__ x, const typename T::S* __restrict__ w,
     typename T::S* __restrict__ y, int64_t rows, int cols, float eps) {
@@ -48,7 +53,7 @@ __global__ __launch_bounds__(RowGeom<L>::kThreads) void rmsnorm_rows(
 #pragma unroll
   for (int e = 0; e < RowRegs<T, L, VPT>::kE; ++e) ss += T::rnd(r.f[e] * r.f[e]);
   ss = group_reduce<L, 0>(ss, red);
-  const float inv = RmsStats<T>::inv_rms(ss, cols, eps);
+  const float inv = RmsStats<T, FORM>::scale(ss, cols, eps);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     const int idx = gl + j * L;
@@ -63,7 +68,7 @@ __global__ __launch_bounds__(RowGeom<L>::kThreads) void rmsnorm_rows(
   }
 }
 
-template <typename T>
+template <typename T, int FORM>
 __global__ __launch_bounds__(kLoopThreads) void rmsnorm_loop(
     const typename T::S* __restrict__ x, const typename T::S* __restrict__ w,
     typename T::S* __restrict__ y, int cols, float eps) {
@@ -76,12 +81,12 @@ __global__ __launch_bounds__(kLoopThreads) void rmsnorm_loop(
     ss += T::rnd(v * v);
   }
   ss = block_reduce<0>(ss, red);
-  const float inv = RmsStats<T>::inv_rms(ss, cols, eps);
+  const float inv = RmsStats<T, FORM>::scale(ss, cols, eps);
   for (int c = threadIdx.x; c < cols; c += kLoopThreads)
     yr[c] = T::from_f(T::rnd(T::to_f(xr[c]) * inv) * T::to_f(w[c]));
 }
 
-template <typename T>
+template <typename T, int FORM>
 static int launch_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int64_t cols,
                           float eps, hipStream_t s) {
   using S = typename T::S;
@@ -94,10 +99,10 @@ static int launch_rmsnorm(const void* x, const void* w, void* y, int64_t rows, i
   if (vec && plan_row(cols / T::kVec, T::kVec, &plan)) {
     AK_ROW_SWITCH({
       const dim3 grid((unsigned)cdiv(rows, RowGeom<L>::kRowsPerBlock));
-      rmsnorm_rows<T, L, VPT><<<grid, RowGeom<L>::kThreads, 0, s>>>(xp, wp, yp, rows, (int)cols, eps);
+      rmsnorm_rows<T, L, VPT, FORM><<<grid, RowGeom<L>::kThreads, 0, s>>>(xp, wp, yp, rows, (int)cols, eps);
     });
   }
-  if (!handled) rmsnorm_loop<T><<<(unsigned)rows, kLoopThreads, 0, s>>>(xp, wp, yp, (int)cols, eps);
+  if (!handled) rmsnorm_loop<T, FORM><<<(unsigned)rows, kLoopThreads, 0, s>>>(xp, wp, yp, (int)cols, eps);
   return record_launch();
 }
 
@@ -501,7 +506,15 @@ extern "C" int ak_rmsnorm(int dtype, const void* x, const void* w, void* y, int6
   if (bad_rows(rows, cols)) return AK_EINVAL;
   if (rows == 0 || cols == 0) return AK_OK;
   if (!x || !w || !y) return AK_EINVAL;
-  AK_DISPATCH(dtype, T, return launch_rmsnorm<T>(x, w, y, rows, cols, eps, stream));
+  AK_DISPATCH(dtype, T, return launch_rmsnorm<T, 0>(x, w, y, rows, cols, eps, stream));
+}
+
+extern "C" int ak_rmsnorm_rsqrt(int dtype, const void* x, const void* w, void* y, int64_t rows,
+                                int64_t cols, float eps, hipStream_t stream) {
+  if (bad_rows(rows, cols)) return AK_EINVAL;
+  if (rows == 0 || cols == 0) return AK_OK;
+  if (!x || !w || !y) return AK_EINVAL;
+  AK_DISPATCH(dtype, T, return launch_rmsnorm<T, 1>(x, w, y, rows, cols, eps, stream));
 }
 
 extern "C" int ak_layernorm(int dtype, const void* x, const void* w, const void* b, void* y,

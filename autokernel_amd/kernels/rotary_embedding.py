@@ -68,16 +68,19 @@ def kernel_fn(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Te
 
 def apply_fp32_tables(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
     """A LLaMA block's RoPE (models/llama_7b.py:40-48) on x [B, T, H, D]: fp32 tables [>= T, D/2],
-    fp32 arithmetic, one rounding to x's dtype. Runs ak_rope_f32_tables."""
+    fp32 arithmetic, one rounding to x's dtype. x may be a column slice of a wider projection
+    output (head and dim contiguous, any token stride). Returns a dense [B, T, H, D] tensor.
+    Runs ak_rope_f32_tables."""
     _lib.require_gpu("rope_fp32_tables", x, cos, sin)
     B, T, H, D = x.shape
     code = _lib.dtype_code(x, "rope_fp32_tables")
-    xc = x.contiguous()
+    if not (x.stride(3) == 1 and x.stride(2) == D and x.stride(0) == T * x.stride(1)):
+        x = x.contiguous()
     c = cos[:T].float().contiguous()
     s = sin[:T].float().contiguous()
-    y = torch.empty_like(xc)
+    y = torch.empty((B, T, H, D), device=x.device, dtype=x.dtype)
     with device_guard(x):
-        st = _lib.load().ak_rope_f32_tables(code, xc.data_ptr(), c.data_ptr(), s.data_ptr(), y.data_ptr(),
-                                            B * T * H, D, T, H, _lib.stream_of(x))
+        st = _lib.load().ak_rope_f32_tables(code, x.data_ptr(), c.data_ptr(), s.data_ptr(), y.data_ptr(),
+                                            B * T * H, D, T, H, x.stride(1), _lib.stream_of(x))
     _lib.check(st, "ak_rope_f32_tables", shape=tuple(x.shape), dtype=x.dtype)
     return y

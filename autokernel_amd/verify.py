@@ -10,9 +10,11 @@ Runs the stock forward, swaps modules for libak355-backed wrappers, reruns, comp
 Replacement strategies (the reference has matmul, layernorm and rmsnorm, verify.py:557-637;
 rotary embedding, attention and the SwiGLU MLP are added here):
   matmul            every nn.Linear -> x @ W.T through ak_gemm reading W in place (no per-call
-                    weight.t().contiguous() copy, verify.py:429)
+                    weight.t().contiguous() copy, verify.py:429); inside attention one fused
+                    QKV GEMM
   layernorm         nn.LayerNorm -> ak_layernorm
-  rmsnorm           RMSNorm-like modules (by class name, or weight + eps, no bias, "...norm") -> ak_rmsnorm
+  rmsnorm           RMSNorm-like modules (by class name, or weight + eps, no bias, "...norm") ->
+                    ak_rmsnorm_rsqrt for class RMSNorm (the model's rsqrt form), else ak_rmsnorm
   rotary_embedding  inside attention: RoPE through ak_rope_f32_tables
   flash_attention   attention modules (wq / wk / wv / wo, n_heads, n_kv_heads) -> GQA-native
                     ak_flash_attn_fwd on strided [B, T, H, D] views (no repeat_interleave, no
@@ -36,6 +38,7 @@ from . import kernels
 from .kernels import flash_attention as fa_mod
 from .kernels import rotary_embedding as rope_mod
 from .kernels.matmul import gemm
+from .kernels.rmsnorm import rms_norm_rsqrt
 
 ALL_KERNELS = ("matmul", "rmsnorm", "layernorm", "rotary_embedding", "flash_attention", "fused_mlp")
 WARMUP_RUNS = 10
@@ -81,14 +84,21 @@ class LayerNormWrapper(nn.Module):
 
 
 class RMSNormWrapper(nn.Module):
+    """RMSNorm-like module -> libak355. A module of class `RMSNorm` computes
+    x * rsqrt(mean(x^2) + eps) * w (the reference's models/llama_7b.py:28-30 and llama.py), which
+    ak_rmsnorm_rsqrt reproduces op for op; other classes get reference.py's form (kernel_fn)."""
+
     def __init__(self, original: nn.Module):
         super().__init__()
         self.original = original
         self.weight = getattr(original, "weight", None)
         self.eps = getattr(original, "eps", 1e-6)
+        self.model_form = type(original).__name__ == "RMSNorm"
 
     def forward(self, x):
         w = self.weight if self.weight is not None else torch.ones(x.shape[-1], device=x.device, dtype=x.dtype)
+        if self.model_form:
+            return rms_norm_rsqrt(x, w, self.eps)
         return kernels.get("rmsnorm")(x, w, self.eps)
 
 
@@ -125,6 +135,12 @@ class AttentionWrapper(nn.Module):
         self.use_rope, self.use_fa, self.use_matmul = use_rope, use_fa, use_matmul
         o = original
         self.n_heads, self.n_kv_heads, self.head_dim = o.n_heads, o.n_kv_heads, o.head_dim
+        # One [H*D + 2*Hk*D, dim] weight for the three projections (copied once, inference only):
+        # one GEMM instead of three, and q / k / v are column slices of its output.
+        self.w_qkv = None
+        if use_matmul and all(getattr(o, n).bias is None for n in ("wq", "wk", "wv")):
+            with torch.no_grad():
+                self.w_qkv = torch.cat([o.wq.weight, o.wk.weight, o.wv.weight], 0).contiguous()
 
     def _proj(self, lin: nn.Linear, x):
         return _linear(x, lin.weight, lin.bias) if self.use_matmul else lin(x)
@@ -133,9 +149,15 @@ class AttentionWrapper(nn.Module):
         o = self.original
         B, T, _ = x.shape
         H, Hk, D = self.n_heads, self.n_kv_heads, self.head_dim
-        q = self._proj(o.wq, x).view(B, T, H, D)
-        k = self._proj(o.wk, x).view(B, T, Hk, D)
-        v = self._proj(o.wv, x).view(B, T, Hk, D)
+        if self.w_qkv is not None:
+            qkv = gemm(x.reshape(B * T, -1), self.w_qkv.t())
+            q = qkv[:, : H * D].view(B, T, H, D)
+            k = qkv[:, H * D: (H + Hk) * D].view(B, T, Hk, D)
+            v = qkv[:, (H + Hk) * D:].view(B, T, Hk, D)
+        else:
+            q = self._proj(o.wq, x).view(B, T, H, D)
+            k = self._proj(o.wk, x).view(B, T, Hk, D)
+            v = self._proj(o.wv, x).view(B, T, Hk, D)
         cos, sin = _rope_tables_from(rope_args)
         if self.use_rope:
             q = rope_mod.apply_fp32_tables(q, cos, sin)

@@ -155,6 +155,8 @@ def op_table():
 
 
 def e2e(timed: int = 20, warm: int = 3):
+    """LLaMA-7B-shaped forward [1, 2048] f16: stock PyTorch vs every op through libak355, both
+    also compared against the same weights run in fp32 (the model's own f16 noise level)."""
     import torch
     from autokernel_amd import llama, verify
     dev = torch.device("cuda:0")
@@ -164,10 +166,20 @@ def e2e(timed: int = 20, warm: int = 3):
     with verify.OptimizedModelContext(model, verify.ALL_KERNELS) as m:
         opt_out, opt_ms = verify.benchmark_model(m, ids, warm, timed)
     cmp = verify.compare_outputs(ref_out, opt_out, torch.float16, 1e-2, 1e-2)
-    res = {"model": "LlamaModel7B (GQA 32/8 heads, FFN 11008, vocab 32000), random N(0,0.02) init",
+    with torch.no_grad():
+        m32 = llama.build("7b", torch.float32, dev)
+        for p16, p32 in zip(model.parameters(), m32.parameters()):
+            p32.copy_(p16.float())
+        out32 = m32(ids).float()
+    del m32
+    e_stock = (ref_out.float() - out32).abs()
+    e_ak = (opt_out.float() - out32).abs()
+    res = {"model": "LlamaModel7B (GQA 32/8 heads, FFN 11008, vocab 32000), random N(0,0.02) init, seed 0",
            "input": [1, 2048], "dtype": "f16", "torch_ms": round(ref_ms, 3), "ak_ms": round(opt_ms, 3),
-           "speedup": round(ref_ms / opt_ms, 3), "correctness_1e-2": cmp["correctness"],
-           "max_abs_error": cmp.get("max_abs_error")}
+           "speedup": round(ref_ms / opt_ms, 3),
+           "vs_stock_allclose_1e-2": cmp["correctness"], "vs_stock_max_abs": cmp.get("max_abs_error"),
+           "stock_vs_fp32_max_abs": round(e_stock.max().item(), 5), "stock_vs_fp32_mean_abs": round(e_stock.mean().item(), 6),
+           "ak_vs_fp32_max_abs": round(e_ak.max().item(), 5), "ak_vs_fp32_mean_abs": round(e_ak.mean().item(), 6)}
     del model
     torch.cuda.empty_cache()
     return res

@@ -61,6 +61,14 @@ int ak_rmsnorm(int dtype, const void* x, const void* w, void* y,
                int64_t rows, int64_t cols, float eps, hipStream_t stream);
 
 /*
+ * RMSNorm in the form a LLaMA block's module computes it: y = x * rsqrt(mean(x*x) + eps) * w,
+ * each step a tensor op rounded to the element type (the rsqrt factor included).
+ * Replaces: models/llama_7b.py:28-30 RMSNorm.forward (the model plug-in's norm replacement).
+ */
+int ak_rmsnorm_rsqrt(int dtype, const void* x, const void* w, void* y,
+                     int64_t rows, int64_t cols, float eps, hipStream_t stream);
+
+/*
  * LayerNorm over the last dim with fp32 statistics: y = (x - mean) * rsqrt(var + eps) * w + b.
  * w or b may be NULL (treated as ones / zeros). x, y: [rows, cols]; w, b: [cols].
  * Replaces: reference.py:20-23 layernorm_ref; kernels/cuda/layernorm.py:268-307 layernorm_cuda.
@@ -88,13 +96,16 @@ int ak_rope(int dtype, const void* x, const void* cos_t, const void* sin_t, void
 
 /*
  * Rotary embedding in the form a LLaMA block applies it: x (f16 / bf16) rotated by fp32 tables
- * with fp32 arithmetic and one rounding to x's dtype; cos_t, sin_t: fp32 [table_rows, head_dim/2];
- * same row-to-table mapping as ak_rope. head_dim a multiple of 8, 16-byte aligned x and y.
+ * with fp32 arithmetic and one rounding to x's dtype; cos_t, sin_t: fp32 [table_rows, head_dim/2].
+ * x holds rows / rep_inner tokens of rep_inner heads; token t starts at element t * x_tok_stride
+ * (rep_inner * head_dim when dense; larger for a column slice of a fused QKV projection) and
+ * uses table row t % table_rows. y is dense [rows, head_dim]. head_dim and x_tok_stride multiples
+ * of 8, x and y 16-byte aligned.
  * Replaces: models/llama_7b.py:40-48 apply_rotary_emb (complex multiply in fp32, type_as(x)).
  */
 int ak_rope_f32_tables(int dtype, const void* x, const float* cos_t, const float* sin_t, void* y,
                        int64_t rows, int64_t head_dim, int64_t table_rows, int64_t rep_inner,
-                       hipStream_t stream);
+                       int64_t x_tok_stride, hipStream_t stream);
 
 /*
  * Mean cross-entropy over rows: out = mean_r( logsumexp(x_r) - x_r[t_r] ), rows whose target is

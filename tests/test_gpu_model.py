@@ -24,3 +24,23 @@ def test_small_llama_all_ops(gpu, kinds):
             out = pm(ids)
     c = verify.compare_outputs(ref, out, torch.float16, 1e-2, 1e-2)
     assert c["correctness"] == "PASS", (kinds, c)
+
+
+def test_model_form_norm_and_strided_rope(gpu):
+    from autokernel_amd.kernels.rmsnorm import rms_norm_rsqrt
+    from autokernel_amd.kernels.rotary_embedding import apply_fp32_tables
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(3, 40, 512, generator=g).half()
+    norm = llama.RMSNorm(512).half()
+    with torch.no_grad():
+        norm.weight.copy_((1 + 0.1 * torch.randn(512, generator=g)).half())
+        exp = norm(x)
+    out = rms_norm_rsqrt(x.to(gpu), norm.weight.to(gpu), norm.eps).cpu()
+    assert (out.float() - exp.float()).abs().max().item() <= 2e-3 * max(1.0, exp.abs().max().item())
+    # q / k as column slices of a fused projection output (token stride 768 > 8 heads * 64)
+    qkv = torch.randn(2, 50, 768, generator=g).half()
+    q = qkv[..., :512].view(2, 50, 8, 64)
+    cos, sin = llama.rope_tables(64, 64)
+    eq, _ = llama.apply_rotary_emb(q, q, cos, sin)
+    oq = apply_fp32_tables(qkv.to(gpu)[..., :512].view(2, 50, 8, 64), cos.to(gpu), sin.to(gpu)).cpu()
+    assert (oq.float() - eq.float()).abs().max().item() <= 1e-3
