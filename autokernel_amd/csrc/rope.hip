@@ -23,7 +23,10 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
 
 // Each thread rotates kCpt 16-byte chunks spaced one grid apart, issuing all loads before any
 // arithmetic so a wave keeps kCpt x 1 KB of x in flight.
-constexpr int kRopeCpt = 4;
+#ifndef AK_ROPE_CPT
+#define AK_ROPE_CPT 1
+#endif
+constexpr int kRopeCpt = AK_ROPE_CPT;
 
 template <typename T>
 __device__ __forceinline__ u32x4 rope_chunk(const u32x4& xv, const typename T::S* cp, const typename T::S* sp) {
