@@ -320,21 +320,143 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma(
 // --------------------------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void;
 
-#ifndef AK_GEMM_STEP_FENCE
-#define AK_GEMM_STEP_FENCE 1
-#endif
-constexpr bool kStepFence = AK_GEMM_STEP_FENCE != 0;
 
 // One LDS-DMA transfer: each lane moves 16 bytes from g to lds_row_base + lane * 16. Kept out of
 // the kernel's lambdas: the device-only builtin there makes the host pass drop the kernel stubs.
 __device__ __forceinline__ void dma16(const uint16_t* g, uint16_t* lds_row_base) {
   __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_row_base, 16, 0, 0);
 }
+// Same from a wave-uniform base plus a per-lane 32-bit byte offset (scalar base + vector offset
+// addressing: one VGPR per transfer instead of a 64-bit address).
+__device__ __forceinline__ void dma16_off(const char* base, uint32_t off, uint16_t* lds_row_base) {
+  __builtin_amdgcn_global_load_lds(base + off, (lds_void*)lds_row_base, 16, 0, 0);
+}
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 16, "vmcnt field");
-  __builtin_amdgcn_s_waitcnt(N | (0x7 << 4) | (0xf << 8));  // vmcnt(N), expcnt / lgkmcnt untouched
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  // vmcnt(N) (bits 3:0 and 15:14), expcnt / lgkmcnt at their maxima (no wait)
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// The k-loop of gemm_dma. The four LDS stage buffers come in as __restrict__ parameters: once
+// inlined, every LDS access carries alias-scope metadata naming its stage, so the compiler's
+// wait-count pass sees that fragment reads of one stage do not alias the DMA still filling the
+// other and does not stall them on vmcnt(0). (Without it, each ds_read after a DMA issue waits for
+// that DMA, which serialises the pipeline.)
+//
+// Fragment pipeline over k-steps (32 k each, two per tile). Each step multiplies the fragments
+// already in registers in two halves (A rows [0, H) then [H, FM)); between the halves it loads the
+// next step's A rows [0, H) and B, after them the remaining A rows. The barrier that retires a
+// stage sits between the halves of a tile's last step, so the second half's MFMAs (operands
+// already in registers) cover the barrier and the next DMA issue.
+template <typename T, int BM, int BN, int WM, int WN, int NB>
+__device__ __forceinline__ void gemm_dma_kloop(
+    f32x4 (&acc)[NB][BM / WM / 16][BN / WN / 16], const uint16_t* A, const uint16_t* B0,
+    const uint16_t* B1, const uint32_t* oa, const uint32_t* ob, int K, int wid, int wm, int wn,
+    int lane, uint16_t* __restrict__ sa0, uint16_t* __restrict__ sa1, uint16_t* __restrict__ sb0,
+    uint16_t* __restrict__ sb1) {
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int A_INS = BM / 8 / NW;
+  constexpr int B_INS = BN / 8 / NW;
+  constexpr int INS = A_INS + NB * B_INS;
+  constexpr int H = FM / 2;
+  const uint16_t* Bm[2] = {B0, B1};
+  const int fr = lane & 15, fc = lane >> 4;
+
+  // k is folded into the 32-bit offset (not the base) so the address stays base + zext(offset).
+  auto issue = [&](int k0, uint16_t* sa, uint16_t* sb) {
+    const uint32_t kb = 2u * (uint32_t)k0;
+#pragma unroll
+    for (int i = 0; i < A_INS; ++i)
+      dma16_off(reinterpret_cast<const char*>(A), oa[i] + kb, sa + (i * NW + wid) * 8 * kBK);
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int i = 0; i < B_INS; ++i)
+        dma16_off(reinterpret_cast<const char*>(Bm[b]), ob[i] + kb,
+                  sb + b * BN * kBK + (i * NW + wid) * 8 * kBK);
+  };
+
+  u32x4 fa[FM], fb[NB][FN], fbn[NB][FN];
+  auto load_a = [&](const uint16_t* sa, int s, int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+      fa[i] = *reinterpret_cast<const u32x4*>(&sa[lds_off_dma(wm * WTM + i * 16 + fr, s * 4 + fc)]);
+  };
+  auto load_b = [&](const uint16_t* sb, int s, u32x4 (*dst)[FN]) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        dst[b][j] = *reinterpret_cast<const u32x4*>(
+            &sb[b * BN * kBK + lds_off_dma(wn * WTN + j * 16 + fr, s * 4 + fc)]);
+  };
+  auto mfma_rows = [&](int i0, int i1) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int i = i0; i < i1; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[b][i][j] = mfma16x16x32<T>(fb[b][j], fa[i], acc[b][i][j]);
+  };
+  const int KT = K / kBK;
+  // One k-step. Next fragments come from (nsa, nsb) step ns when has_next. cross: this is the
+  // tile's last step, so wait for the other stage's DMA and retire this stage at a barrier; dma:
+  // then refill it with tile dma_kt. Every flag is a literal at its call site, so the main loop
+  // has no branches (a conditional DMA issue there costs an extra vmcnt wait at the loop head).
+  auto kstep = [&](const uint16_t* nsa, const uint16_t* nsb, int ns, bool has_next, bool cross,
+                   bool dma, int dma_kt, uint16_t* dsa, uint16_t* dsb) {
+    mfma_rows(0, H);
+    __builtin_amdgcn_sched_barrier(0);
+    if (cross) {
+      wait_vmcnt<0>();
+      __syncthreads();
+      if (dma) issue(dma_kt * kBK, dsa, dsb);
+    }
+    if (has_next) {
+      load_a(nsa, ns, 0, H);
+      load_b(nsb, ns, fbn);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_rows(H, FM);
+    __builtin_amdgcn_sched_barrier(0);
+    if (has_next) {
+      load_a(nsa, ns, H, FM);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) fb[b][j] = fbn[b][j];
+    }
+  };
+
+  issue(0, sa0, sb0);
+  if (KT > 1) {
+    issue(kBK, sa1, sb1);
+    wait_vmcnt<INS>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  __syncthreads();
+  load_a(sa0, 0, 0, FM);
+  load_b(sb0, 0, fb);
+  // Tile kt sits in stage 0 and tile kt + 1 is in flight to stage 1. Past the last tile the refill
+  // DMA re-fetches tile KT - 1 into the retired stage, which is never read again: the loop body
+  // stays branch-free at the cost of one redundant tile per block.
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    kstep(sa0, sb0, 1, true, false, false, 0, sa0, sb0);                      // tile kt, step 0
+    kstep(sa1, sb1, 0, true, true, true, min(kt + 2, KT - 1), sa0, sb0);      // tile kt, step 1
+    kstep(sa1, sb1, 1, true, false, false, 0, sa1, sb1);                      // tile kt + 1, step 0
+    kstep(sa0, sb0, 0, true, true, true, min(kt + 3, KT - 1), sa1, sb1);      // tile kt + 1, step 1
+  }
+  if (kt < KT) {  // odd tile count: the last tile sits in stage 0
+    kstep(sa0, sb0, 1, true, false, false, 0, sa0, sb0);
+    kstep(sa0, sb0, 0, false, false, false, 0, sa0, sb0);
+  }
+  wait_vmcnt<0>();  // no DMA may still target this block's LDS when its waves end
 }
 
 template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI>
@@ -348,48 +470,37 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
   constexpr int A_INS = BM / 8 / NW;  // DMA instructions per wave per tile for A
   constexpr int B_INS = BN / 8 / NW;  // ... per B matrix
   static_assert(A_INS * 8 * NW == BM && B_INS * 8 * NW == BN, "tile rows split over waves");
-  constexpr int INS = A_INS + NB * B_INS;
-  static_assert(INS < 16, "outstanding DMA per tile fits vmcnt");
+  static_assert(A_INS + NB * B_INS < 64, "outstanding DMA per tile fits vmcnt");
+  static_assert(FM % 2 == 0, "two MFMA halves per k-step");
 
   __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * kBK];
   __shared__ __attribute__((aligned(1024))) uint16_t sA1[BM * kBK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB0[NB][BN * kBK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB1[NB][BN * kBK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB0[NB * BN * kBK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB1[NB * BN * kBK];
 
   int tm, tn;
   tile_coords(tiles_m, tiles_n, &tm, &tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int lane = lane_id(), wid = wave_id();
+  const int lane = lane_id();
+  const int wid = __builtin_amdgcn_readfirstlane(wave_id());  // wave-uniform: LDS bases in SGPRs
   const int wm = wid / WN, wn = wid % WN;
   const int r_in = lane >> 3, pc = lane & 7;
-  const uint16_t* Bm[2] = {B0, B1};
 
-  // Per-lane element offsets (fixed over k; the host guarantees they fit 32 bits) of the row and
-  // chunk each DMA instruction fetches: physical chunk pc of a row holds logical chunk
-  // swz_dma(row, pc) (the XOR pattern is its own inverse).
-  int oa[A_INS];
+  // Per-lane byte offsets (fixed over k; the host guarantees M * lda and N * ldb elements fit
+  // 31 bits, so bytes fit 32) of the row and chunk each DMA instruction fetches: physical chunk pc
+  // of a row holds logical chunk swz_dma(row, pc) (the XOR pattern is its own inverse).
+  uint32_t oa[A_INS];
 #pragma unroll
   for (int i = 0; i < A_INS; ++i) {
     const int row = (i * NW + wid) * 8 + r_in;
-    oa[i] = min(m0 + row, M - 1) * (int)lda + swz_dma(row, pc) * 8;
+    oa[i] = 2u * (uint32_t)(min(m0 + row, M - 1) * (int)lda + swz_dma(row, pc) * 8);
   }
-  int ob[B_INS];
+  uint32_t ob[B_INS];
 #pragma unroll
   for (int i = 0; i < B_INS; ++i) {
     const int row = (i * NW + wid) * 8 + r_in;
-    ob[i] = min(n0 + row, N - 1) * (int)ldb + swz_dma(row, pc) * 8;
+    ob[i] = 2u * (uint32_t)(min(n0 + row, N - 1) * (int)ldb + swz_dma(row, pc) * 8);
   }
-
-  auto issue = [&](int k0, uint16_t* sa, uint16_t (*sb)[BN * kBK]) {
-#pragma unroll
-    for (int i = 0; i < A_INS; ++i)
-      dma16(A + (oa[i] + k0), sa + (i * NW + wid) * 8 * kBK);
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int i = 0; i < B_INS; ++i)
-        dma16(Bm[b] + (ob[i] + k0), sb[b] + (i * NW + wid) * 8 * kBK);
-  };
 
   f32x4 acc[NB][FM][FN];
 #pragma unroll
@@ -399,52 +510,9 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[b][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  gemm_dma_kloop<T, BM, BN, WM, WN, NB>(acc, A, B0, B1, oa, ob, K, wid, wm, wn, lane, sA0, sA1, sB0, sB1);
+
   const int fr = lane & 15, fc = lane >> 4;
-  auto compute = [&](const uint16_t* sa, const uint16_t (*sb)[BN * kBK]) {
-#pragma unroll
-    for (int s = 0; s < kBK / 32; ++s) {
-      u32x4 fa[FM], fb[NB][FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        fa[i] = *reinterpret_cast<const u32x4*>(&sa[lds_off_dma(wm * WTM + i * 16 + fr, s * 4 + fc)]);
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          fb[b][j] = *reinterpret_cast<const u32x4*>(&sb[b][lds_off_dma(wn * WTN + j * 16 + fr, s * 4 + fc)]);
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int j = 0; j < FN; ++j) acc[b][i][j] = mfma16x16x32<T>(fb[b][j], fa[i], acc[b][i][j]);
-      // Optionally keep the next k-step's fragment loads below these MFMAs.
-      if constexpr (kStepFence) __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-
-  const int KT = K / kBK;
-  issue(0, sA0, sB0);
-  if (KT > 1) {
-    issue(kBK, sA1, sB1);
-    wait_vmcnt<INS>();
-  } else {
-    wait_vmcnt<0>();
-  }
-  __syncthreads();
-  int kt = 0;
-  for (; kt + 1 < KT; kt += 2) {
-    compute(sA0, sB0);  // tile kt (stage 0)
-    wait_vmcnt<0>();    // tile kt + 1 has landed in stage 1
-    __syncthreads();    // ... for every wave, and stage 0 is no longer read
-    if (kt + 2 < KT) issue((kt + 2) * kBK, sA0, sB0);
-    compute(sA1, sB1);  // tile kt + 1 (stage 1)
-    wait_vmcnt<0>();
-    __syncthreads();
-    if (kt + 3 < KT) issue((kt + 3) * kBK, sA1, sB1);
-  }
-  if (kt < KT) compute(sA0, sB0);  // odd tile count: the last tile sits in stage 0
-
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int m = m0 + wm * WTM + i * 16 + fr;
@@ -678,11 +746,11 @@ static void launch_gemm_dma(const void* A, const void* B0, const void* B1, void*
                             int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
   const TileCfg t = pick_tile(M, N, NB);
   if constexpr (NB == 1) {
-    if (t.bm == 256 && t.bn == 256) launch_dma_cfg<T, 256, 256, 2, 4, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+    if (t.bm == 256 && t.bn == 256) launch_dma_cfg<T, 256, 256, 2, kBigWN, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
     else if (t.bm == 256) launch_dma_cfg<T, 256, 128, 4, 2, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
     else launch_dma_cfg<T, 128, 128, 2, 2, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
   } else {
-    if (t.bm == 256 && t.bn == 256) launch_dma_cfg<T, 256, 128, 2, 4, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+    if (t.bm == 256 && t.bn == 256) launch_dma_cfg<T, 256, 128, 2, kBigWN, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
     else if (t.bm == 256) launch_dma_cfg<T, 256, 64, 4, 2, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
     else launch_dma_cfg<T, 128, 64, 2, 2, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
   }
