@@ -2,18 +2,18 @@
 // SwiGLU gate/up kernel built on it, and a full-precision fp32 GEMM on v_mfma_f32_16x16x4_f32.
 //
 // f16 / bf16 design
-//   * Block tile BM x BN x 64 (BN per B matrix; NB = 1 plain GEMM, NB = 2 gate and up sharing
-//     the A tile). WM x WN waves; each wave owns a (BM/WM) x (BN/WN) sub-tile per B matrix made of
-//     16x16 v_mfma_f32_16x16x32_{f16,bf16} tiles.
-//   * Both operands sit in LDS K-contiguous, [rows][64] elements, 16-byte chunks XOR-swizzled by
-//     (row & 7) so the 16 rows read by one MFMA fragment load hit distinct banks.
-//   * B given as [K, N] (torch.matmul layout) is transposed in registers on its way to LDS:
-//     each thread loads an 8(k) x 8(n) block with eight 16-byte loads and rebuilds it as eight
-//     K-contiguous 16-byte rows with v_perm_b32. nn.Linear weights ([N, K]) load directly.
-//   * The MFMA is issued with B as the "A" operand, so the accumulator of a lane holds four
-//     consecutive C columns of one row (8-byte stores in the epilogue).
-//   * Two LDS stages with register prefetch: the global loads of tile k+1 are in flight while
-//     tile k is multiplied; one barrier per k-tile.
+//   * Block tile BM x BN (BN per B matrix; NB = 1 plain GEMM, NB = 2 gate and up sharing the A
+//     tile). WM x WN waves; each wave owns a (BM/WM) x (BN/WN) sub-tile per B matrix made of
+//     16x16 v_mfma_f32_16x16x32_{f16,bf16} tiles. The MFMA is issued with B as the "A" operand,
+//     so a lane's accumulator holds four consecutive C columns of one row (8-byte stores).
+//   * Main kernel (gemm_dma, K-contiguous B = nn.Linear weights, K % 64 == 0): operands reach LDS
+//     by LDS DMA, two or three 64-deep stages (four 32-deep ones when the grid under-fills the
+//     chip), so one or two tiles stream in while one is multiplied. Inside a tile the next
+//     k-step's fragments load from LDS while the current MFMAs run, and the barrier that retires
+//     a stage sits between the two halves of a k-step's MFMAs.
+//   * Fallback kernel (gemm_mfma: any alignment, odd K, strided or [K, N] B): register-staged
+//     loads into two LDS stages of [rows][64], chunks XOR-swizzled; [K, N] B is transposed in
+//     registers on its way to LDS (8x8 blocks rebuilt as K-contiguous rows with v_perm_b32).
 //   * Tile order is XCD-aware: hardware hands block i to XCD i % 8, so consecutive logical tiles
 //     are given to one XCD and grouped along M to share A and B in that XCD's L2.
 #include <limits.h>
@@ -30,20 +30,6 @@ constexpr int kKC = kBK / 8;      // 16-byte chunks per tile row
 __device__ __forceinline__ int swz(int row, int c) { return c ^ ((row ^ (row >> 3)) & 7); }
 // element offset of chunk c of row `row` in a [rows][64] tile
 __device__ __forceinline__ int lds_off(int row, int c) { return row * kBK + swz(row, c) * 8; }
-// Swizzle for tiles written by LDS DMA (whole 8-row groups at once). gfx950 serves a 64-lane
-// ds_read_b128 in 8-lane phases of 128 bytes, so chunk c ^ (row & 7) makes the 8 rows of a phase
-// hit 8 different 16-byte slots (measured: SQ_LDS_BANK_CONFLICT 0 vs 50% for a variant with an
-// extra row-bit-3 term, 75% unswizzled). The pattern does not depend on which 16-row fragment is
-// read, so fragment addresses are one base register plus immediate offsets.
-#ifndef AK_GEMM_DMA_SWZ
-#define AK_GEMM_DMA_SWZ 2
-#endif
-__device__ __forceinline__ int swz_dma(int row, int c) {
-  if constexpr (AK_GEMM_DMA_SWZ == 1) return c ^ ((row & 7) ^ ((row >> 3) & 1));
-  else if constexpr (AK_GEMM_DMA_SWZ == 2) return c ^ (row & 7);
-  else return c;
-}
-__device__ __forceinline__ int lds_off_dma(int row, int c) { return row * kBK + swz_dma(row, c) * 8; }
 
 template <typename T>
 __device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c);
@@ -311,25 +297,35 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma(
 // --------------------------------------------------------------------------------------------
 // The f16 / bf16 kernel for K-contiguous B ([N, K], nn.Linear weights) with K % 64 == 0.
 // Tiles move global -> LDS with gfx950's LDS DMA (global_load_lds_dwordx4): no staging registers
-// and no LDS store instructions. One DMA instruction writes 64 lanes x 16 bytes = 8 consecutive
-// tile rows; lane L fills physical chunk L % 8 of row L / 8, so it fetches the logical chunk that
-// the XOR swizzle maps there. Rows past M / N are clamped to the last row (their results are
-// never stored). Two LDS stages live in separate arrays and the k loop is unrolled by two, so the
-// stage being read and the stage being filled are distinct objects; tile k+2 streams in while
-// tile k+1 is multiplied. One barrier per k-tile.
+// and no LDS store instructions. One DMA instruction writes 64 lanes x 16 bytes = 1 KB of
+// consecutive tile rows; each lane fetches the logical chunk that the XOR swizzle maps to its
+// physical slot. Rows past M / N are clamped to the last row (their results are never stored).
+// gfx950 serves a 64-lane ds_read_b128 in 8-lane phases, so the swizzles put the 8 rows of a phase
+// in 8 distinct 16-byte bank slots (measured for 128-byte rows: SQ_LDS_BANK_CONFLICT 0 with
+// chunk c ^ (row & 7), 50% with an extra row-bit-3 term, 75% unswizzled).
 // --------------------------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void;
 
+// Barrier for the DMA pipelines: this wave's DMA transfers older than the newest N have landed
+// and its own LDS reads have returned, then s_barrier. No memory-model fence: a workgroup release
+// fence would also wait for the newest DMA transfers (they write LDS), collapsing the pipeline to
+// one tile in flight. The signal fences keep the compiler from moving memory accesses across.
+template <int N>
+__device__ __forceinline__ void dma_barrier();
 
-// One LDS-DMA transfer: each lane moves 16 bytes from g to lds_row_base + lane * 16. Kept out of
-// the kernel's lambdas: the device-only builtin there makes the host pass drop the kernel stubs.
-__device__ __forceinline__ void dma16(const uint16_t* g, uint16_t* lds_row_base) {
-  __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_row_base, 16, 0, 0);
-}
-// Same from a wave-uniform base plus a per-lane 32-bit byte offset (scalar base + vector offset
-// addressing: one VGPR per transfer instead of a 64-bit address).
-__device__ __forceinline__ void dma16_off(const char* base, uint32_t off, uint16_t* lds_row_base) {
-  __builtin_amdgcn_global_load_lds(base + off, (lds_void*)lds_row_base, 16, 0, 0);
+// The same transfer as inline assembly. The compiler then does not track it: its wait-count pass
+// inserts no waits for it (a conservative full wait at a loop head otherwise drains the whole
+// four-stage pipeline once per iteration), and every wait is the caller's explicit vmcnt. M0
+// holds the wave-uniform LDS destination; one wait state separates its write from the load.
+__device__ __forceinline__ void dma16_asm(const char* base, uint32_t off, uint16_t* lds_row_base) {
+  const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)lds_row_base;
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(off), "s"(base), "s"(lds)
+      : "memory", "m0");
 }
 
 template <int N>
@@ -339,60 +335,78 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
-// The k-loop of gemm_dma. The four LDS stage buffers come in as __restrict__ parameters: once
-// inlined, every LDS access carries alias-scope metadata naming its stage, so the compiler's
-// wait-count pass sees that fragment reads of one stage do not alias the DMA still filling the
-// other and does not stall them on vmcnt(0). (Without it, each ds_read after a DMA issue waits for
-// that DMA, which serialises the pipeline.)
-//
-// Fragment pipeline over k-steps (32 k each, two per tile). Each step multiplies the fragments
-// already in registers in two halves (A rows [0, H) then [H, FM)); between the halves it loads the
-// next step's A rows [0, H) and B, after them the remaining A rows. The barrier that retires a
-// stage sits between the halves of a tile's last step, so the second half's MFMAs (operands
-// already in registers) cover the barrier and the next DMA issue.
-template <typename T, int BM, int BN, int WM, int WN, int NB>
-__device__ __forceinline__ void gemm_dma_kloop(
+template <int N>
+__device__ __forceinline__ void dma_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  // vmcnt(N), lgkmcnt(0), expcnt untouched
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4));
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Multi-stage variant: NS LDS stages of BKD-deep tiles (BKD 64: 128-byte rows, chunk c of row r
+// at c ^ (r & 7), 8 rows per DMA instruction; BKD 32: 64-byte rows, chunk c at c ^ ((r >> 2) & 1),
+// 16 rows per instruction; either way the 8 rows of one ds_read_b128 phase hit 8 distinct 16-byte
+// bank slots). NS - 1 tiles are in flight while one is multiplied. Tile t lives in stage t % NS;
+// the loop runs in groups of NS tiles with a uniform guard on the tail.
+template <int BKD>
+struct DmaGeom;
+template <>
+struct DmaGeom<64> {
+  static constexpr int RPI = 8;  // rows per 1 KB DMA instruction
+  __device__ static __forceinline__ int swz(int r, int c) { return c ^ (r & 7); }
+};
+template <>
+struct DmaGeom<32> {
+  static constexpr int RPI = 16;
+  __device__ static __forceinline__ int swz(int r, int c) { return c ^ ((r >> 2) & 1); }
+};
+
+template <typename T, int BM, int BN, int WM, int WN, int NB, int BKD, int NS>
+__device__ __forceinline__ void gemm_dma_ns_kloop(
     f32x4 (&acc)[NB][BM / WM / 16][BN / WN / 16], const uint16_t* A, const uint16_t* B0,
     const uint16_t* B1, const uint32_t* oa, const uint32_t* ob, int K, int wid, int wm, int wn,
-    int lane, uint16_t* __restrict__ sa0, uint16_t* __restrict__ sa1, uint16_t* __restrict__ sb0,
-    uint16_t* __restrict__ sb1) {
+    int lane, uint16_t* s0, uint16_t* s1, uint16_t* s2, uint16_t* s3) {
+  using G = DmaGeom<BKD>;
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
-  constexpr int A_INS = BM / 8 / NW;
-  constexpr int B_INS = BN / 8 / NW;
+  constexpr int A_INS = BM / G::RPI / NW;
+  constexpr int B_INS = BN / G::RPI / NW;
   constexpr int INS = A_INS + NB * B_INS;
   constexpr int H = FM / 2;
+  constexpr int STEPS = BKD / 32;  // k-steps of 32 per tile
+  static_assert(NS >= 2 && NS <= 4, "stages");
   const uint16_t* Bm[2] = {B0, B1};
   const int fr = lane & 15, fc = lane >> 4;
+  uint16_t* const st[4] = {s0, s1, s2, s3};
 
-  // k is folded into the 32-bit offset (not the base) so the address stays base + zext(offset).
-  auto issue = [&](int k0, uint16_t* sa, uint16_t* sb) {
-    const uint32_t kb = 2u * (uint32_t)k0;
+  auto issue = [&](int kt, uint16_t* sp) {
+    const uint32_t kb = 2u * (uint32_t)(kt * BKD);
 #pragma unroll
     for (int i = 0; i < A_INS; ++i)
-      dma16_off(reinterpret_cast<const char*>(A), oa[i] + kb, sa + (i * NW + wid) * 8 * kBK);
+      dma16_asm(reinterpret_cast<const char*>(A), oa[i] + kb, sp + (i * NW + wid) * G::RPI * BKD);
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int i = 0; i < B_INS; ++i)
-        dma16_off(reinterpret_cast<const char*>(Bm[b]), ob[i] + kb,
-                  sb + b * BN * kBK + (i * NW + wid) * 8 * kBK);
+        dma16_asm(reinterpret_cast<const char*>(Bm[b]), ob[i] + kb,
+                  sp + (BM + b * BN) * BKD + (i * NW + wid) * G::RPI * BKD);
   };
-
   u32x4 fa[FM], fb[NB][FN], fbn[NB][FN];
-  auto load_a = [&](const uint16_t* sa, int s, int i0, int i1) {
-#pragma unroll
-    for (int i = i0; i < i1; ++i)
-      fa[i] = *reinterpret_cast<const u32x4*>(&sa[lds_off_dma(wm * WTM + i * 16 + fr, s * 4 + fc)]);
+  auto frag = [&](const uint16_t* base, int row, int s) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(&base[row * BKD + G::swz(row, s * 4 + fc) * 8]);
   };
-  auto load_b = [&](const uint16_t* sb, int s, u32x4 (*dst)[FN]) {
+  auto load_a = [&](const uint16_t* sp, int s, int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i) fa[i] = frag(sp, wm * WTM + i * 16 + fr, s);
+  };
+  auto load_b = [&](const uint16_t* sp, int s, u32x4 (*dst)[FN]) {
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-        dst[b][j] = *reinterpret_cast<const u32x4*>(
-            &sb[b * BN * kBK + lds_off_dma(wn * WTN + j * 16 + fr, s * 4 + fc)]);
+      for (int j = 0; j < FN; ++j) dst[b][j] = frag(sp + (BM + b * BN) * BKD, wn * WTN + j * 16 + fr, s);
   };
   auto mfma_rows = [&](int i0, int i1) {
 #pragma unroll
@@ -402,64 +416,52 @@ __device__ __forceinline__ void gemm_dma_kloop(
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[b][i][j] = mfma16x16x32<T>(fb[b][j], fa[i], acc[b][i][j]);
   };
-  const int KT = K / kBK;
-  // One k-step. Next fragments come from (nsa, nsb) step ns when has_next. cross: this is the
-  // tile's last step, so wait for the other stage's DMA and retire this stage at a barrier; dma:
-  // then refill it with tile dma_kt. Every flag is a literal at its call site, so the main loop
-  // has no branches (a conditional DMA issue there costs an extra vmcnt wait at the loop head).
-  auto kstep = [&](const uint16_t* nsa, const uint16_t* nsb, int ns, bool has_next, bool cross,
-                   bool dma, int dma_kt, uint16_t* dsa, uint16_t* dsb) {
+  const int KT = K / BKD;
+  // One k-step: first half of the MFMAs; at a tile's last step (cross) wait until the next tile
+  // has landed (NS - 2 later tiles may still be in flight), barrier (every wave holds this tile's
+  // fragments, so its stage is free) and refill the stage with tile refill_kt (clamped: past the
+  // end it re-fetches the last tile into a stage nobody reads again); the next step's fragments
+  // load around the second half.
+  auto kstep = [&](const uint16_t* nsp, int ns, bool cross, uint16_t* rsp, int refill_kt) {
     mfma_rows(0, H);
     __builtin_amdgcn_sched_barrier(0);
     if (cross) {
-      wait_vmcnt<0>();
-      __syncthreads();
-      if (dma) issue(dma_kt * kBK, dsa, dsb);
+      dma_barrier<(NS - 2) * INS>();
+      issue(refill_kt, rsp);
     }
-    if (has_next) {
-      load_a(nsa, ns, 0, H);
-      load_b(nsb, ns, fbn);
-    }
+    load_a(nsp, ns, 0, H);
+    load_b(nsp, ns, fbn);
     __builtin_amdgcn_sched_barrier(0);
     mfma_rows(H, FM);
     __builtin_amdgcn_sched_barrier(0);
-    if (has_next) {
-      load_a(nsa, ns, H, FM);
+    load_a(nsp, ns, H, FM);
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) fb[b][j] = fbn[b][j];
-    }
+      for (int j = 0; j < FN; ++j) fb[b][j] = fbn[b][j];
   };
-
-  issue(0, sa0, sb0);
-  if (KT > 1) {
-    issue(kBK, sa1, sb1);
-    wait_vmcnt<INS>();
-  } else {
-    wait_vmcnt<0>();
-  }
-  __syncthreads();
-  load_a(sa0, 0, 0, FM);
-  load_b(sb0, 0, fb);
-  // Tile kt sits in stage 0 and tile kt + 1 is in flight to stage 1. Past the last tile the refill
-  // DMA re-fetches tile KT - 1 into the retired stage, which is never read again: the loop body
-  // stays branch-free at the cost of one redundant tile per block.
-  int kt = 0;
-  for (; kt + 1 < KT; kt += 2) {
-    kstep(sa0, sb0, 1, true, false, false, 0, sa0, sb0);                      // tile kt, step 0
-    kstep(sa1, sb1, 0, true, true, true, min(kt + 2, KT - 1), sa0, sb0);      // tile kt, step 1
-    kstep(sa1, sb1, 1, true, false, false, 0, sa1, sb1);                      // tile kt + 1, step 0
-    kstep(sa0, sb0, 0, true, true, true, min(kt + 3, KT - 1), sa1, sb1);      // tile kt + 1, step 1
-  }
-  if (kt < KT) {  // odd tile count: the last tile sits in stage 0
-    kstep(sa0, sb0, 1, true, false, false, 0, sa0, sb0);
-    kstep(sa0, sb0, 0, false, false, false, 0, sa0, sb0);
+#pragma unroll
+  for (int i = 0; i < NS; ++i) issue(min(i, KT - 1), st[i]);
+  dma_barrier<(NS - 1) * INS>();
+  load_a(s0, 0, 0, FM);
+  load_b(s0, 0, fb);
+  for (int kt = 0; kt < KT; kt += NS) {
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int t = kt + u;
+      if (t < KT) {  // uniform over the block
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+          if (s + 1 < STEPS) kstep(st[u], s + 1, false, st[u], 0);
+          else kstep(st[(u + 1) % NS], 0, true, st[u], min(t + NS, KT - 1));
+        }
+      }
+    }
   }
   wait_vmcnt<0>();  // no DMA may still target this block's LDS when its waves end
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI>
+template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, int BKD, int NS>
 __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B0, const uint16_t* __restrict__ B1,
     uint16_t* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
@@ -467,16 +469,17 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
-  constexpr int A_INS = BM / 8 / NW;  // DMA instructions per wave per tile for A
-  constexpr int B_INS = BN / 8 / NW;  // ... per B matrix
-  static_assert(A_INS * 8 * NW == BM && B_INS * 8 * NW == BN, "tile rows split over waves");
-  static_assert(A_INS + NB * B_INS < 64, "outstanding DMA per tile fits vmcnt");
+  constexpr int RPI = DmaGeom<BKD>::RPI;  // tile rows per DMA instruction (1 KB)
+  constexpr int A_INS = BM / RPI / NW;  // DMA instructions per wave per tile for A
+  constexpr int B_INS = BN / RPI / NW;  // ... per B matrix
+  static_assert(A_INS * RPI * NW == BM && B_INS * RPI * NW == BN, "tile rows split over waves");
+  static_assert(4 * (A_INS + NB * B_INS) < 64, "outstanding DMA fits vmcnt");
   static_assert(FM % 2 == 0, "two MFMA halves per k-step");
-
-  __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * kBK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sA1[BM * kBK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB0[NB * BN * kBK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB1[NB * BN * kBK];
+  constexpr int kStage = (BM + NB * BN) * BKD;  // elements per stage
+  __shared__ __attribute__((aligned(1024))) uint16_t sS0[kStage];
+  __shared__ __attribute__((aligned(1024))) uint16_t sS1[kStage];
+  __shared__ __attribute__((aligned(1024))) uint16_t sS2[NS > 2 ? kStage : 1];
+  __shared__ __attribute__((aligned(1024))) uint16_t sS3[NS > 3 ? kStage : 1];
 
   int tm, tn;
   tile_coords(tiles_m, tiles_n, &tm, &tn);
@@ -484,22 +487,24 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
   const int lane = lane_id();
   const int wid = __builtin_amdgcn_readfirstlane(wave_id());  // wave-uniform: LDS bases in SGPRs
   const int wm = wid / WN, wn = wid % WN;
-  const int r_in = lane >> 3, pc = lane & 7;
+  const int r_in = lane / (64 / RPI), pc = lane % (64 / RPI);
 
   // Per-lane byte offsets (fixed over k; the host guarantees M * lda and N * ldb elements fit
   // 31 bits, so bytes fit 32) of the row and chunk each DMA instruction fetches: physical chunk pc
-  // of a row holds logical chunk swz_dma(row, pc) (the XOR pattern is its own inverse).
+  // of a row holds logical chunk swz(row, pc) (each XOR pattern is its own inverse).
   uint32_t oa[A_INS];
 #pragma unroll
   for (int i = 0; i < A_INS; ++i) {
-    const int row = (i * NW + wid) * 8 + r_in;
-    oa[i] = 2u * (uint32_t)(min(m0 + row, M - 1) * (int)lda + swz_dma(row, pc) * 8);
+    const int row = (i * NW + wid) * RPI + r_in;
+    const int lc = DmaGeom<BKD>::swz(row, pc);
+    oa[i] = 2u * (uint32_t)(min(m0 + row, M - 1) * (int)lda + lc * 8);
   }
   uint32_t ob[B_INS];
 #pragma unroll
   for (int i = 0; i < B_INS; ++i) {
-    const int row = (i * NW + wid) * 8 + r_in;
-    ob[i] = 2u * (uint32_t)(min(n0 + row, N - 1) * (int)ldb + swz_dma(row, pc) * 8);
+    const int row = (i * NW + wid) * RPI + r_in;
+    const int lc = DmaGeom<BKD>::swz(row, pc);
+    ob[i] = 2u * (uint32_t)(min(n0 + row, N - 1) * (int)ldb + lc * 8);
   }
 
   f32x4 acc[NB][FM][FN];
@@ -510,7 +515,8 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[b][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  gemm_dma_kloop<T, BM, BN, WM, WN, NB>(acc, A, B0, B1, oa, ob, K, wid, wm, wn, lane, sA0, sA1, sB0, sB1);
+  gemm_dma_ns_kloop<T, BM, BN, WM, WN, NB, BKD, NS>(acc, A, B0, B1, oa, ob, K, wid, wm, wn, lane, sS0, sS1, sS2,
+                                                    sS3);
 
   const int fr = lane & 15, fc = lane >> 4;
 #pragma unroll
@@ -668,9 +674,12 @@ struct TileCfg {
 
 // Pick the tile that keeps the 256 CUs busiest: fraction of CU-slots doing useful work over the
 // launch, weighted by the per-tile efficiency of smaller tiles (more LDS and L2 traffic per flop).
+#ifndef AK_GEMM_EFF256
+#define AK_GEMM_EFF256 1.0
+#endif
 static TileCfg pick_tile(int64_t M, int64_t N, int nb) {
   const TileCfg cands[] = {{256, 256}, {256, 128}, {128, 128}};
-  const double eff[] = {1.0, 0.92, 0.80};
+  const double eff[] = {AK_GEMM_EFF256, 0.88, 0.80};
   const int cus = 256;
   TileCfg best = cands[2];
   double best_s = -1.0;
@@ -731,14 +740,55 @@ static void launch_gemm_tiled(const void* A, const void* B0, const void* B1, voi
 #define AK_GEMM_DMA 1
 #endif
 constexpr bool kUseDma = AK_GEMM_DMA != 0;
+#ifndef AK_GEMM_DEEP
+#define AK_GEMM_DEEP 1
+#endif
+constexpr bool kUseDeep = AK_GEMM_DEEP != 0;
+constexpr int kCUs = 256;  // MI355X compute units
+
+template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, int BKD, int NS>
+static void launch_dma_kernel(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
+                              int64_t lda, int64_t ldb, int64_t ldc, int tiles_m, int tiles_n, hipStream_t s) {
+  gemm_dma<T, BM, BN, WM, WN, NB, EPI, BKD, NS><<<tiles_m * tiles_n, WM * WN * kWave, 0, s>>>(
+      (const uint16_t*)A, (const uint16_t*)B0, (const uint16_t*)B1, (uint16_t*)C, M, N, K, lda, ldb, ldc,
+      tiles_m, tiles_n);
+}
+
+// Pipeline plan per tile shape: stage bytes (BM + NB * BN) * BKD * 2 and the 160 KB of LDS fix
+// how many stages fit.
+#ifndef AK_GEMM_PLAN
+#define AK_GEMM_PLAN 2
+#endif
+template <int BM, int BN, int NB, int NW>
+struct DmaPlan {
+  static constexpr int kStage64 = (BM + NB * BN) * 64 * 2;
+  static constexpr int kFit64 = 163840 / kStage64;
+  static constexpr bool kOk32 = BM % (16 * NW) == 0 && BN % (16 * NW) == 0;
+  // plan 1: two 64-deep stages; 2 (default): three 64-deep stages where they fit beside 8 waves,
+  // else two; 3: four 32-deep stages. Measured (bf16, NT):
+  // 2048x4096x4096 on 256x128 tiles 83.5 us two-stage -> 63.4 us three-stage; 4096^3 on 256x256
+  // 107.4 us two-stage (plan 3: 121.2 us, the doubled barrier count outweighs the deeper queue).
+  static constexpr int BKD = (AK_GEMM_PLAN == 3 && kOk32) ? 32 : 64;
+  static constexpr int NS = AK_GEMM_PLAN == 1 ? 2
+                            : AK_GEMM_PLAN == 2 ? (kFit64 >= 3 && NW == 8 ? 3 : 2)
+                            : (kOk32 ? 4 : 2);
+};
 
 template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI>
 static void launch_dma_cfg(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
                            int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
   const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(N, BN);
-  gemm_dma<T, BM, BN, WM, WN, NB, EPI><<<tiles_m * tiles_n, WM * WN * kWave, 0, s>>>(
-      (const uint16_t*)A, (const uint16_t*)B0, (const uint16_t*)B1, (uint16_t*)C, M, N, K, lda, ldb, ldc,
-      tiles_m, tiles_n);
+  using P = DmaPlan<BM, BN, NB, WM * WN>;
+  // Four 32-deep stages when the grid leaves CUs idle (fewer tiles than CUs: each block's own DMA
+  // latency is then exposed; measured 2048x1024x4096: 50.9 us against 59.0 us two-stage).
+  constexpr bool kOk32 = P::kOk32;
+  if (kOk32 && kUseDeep && tiles_m * tiles_n < kCUs) {
+    if constexpr (kOk32)
+      launch_dma_kernel<T, BM, BN, WM, WN, NB, EPI, 32, 4>(A, B0, B1, C, M, N, K, lda, ldb, ldc, tiles_m, tiles_n, s);
+    return;
+  }
+  launch_dma_kernel<T, BM, BN, WM, WN, NB, EPI, P::BKD, P::NS>(A, B0, B1, C, M, N, K, lda, ldb, ldc, tiles_m,
+                                                               tiles_n, s);
 }
 
 template <typename T, int NB, int EPI>
