@@ -116,6 +116,34 @@ __device__ __forceinline__ float wave_nan_max(float v) {
   return v;
 }
 
+// ---------------------------------------------------------------------------------------------
+// LDS DMA (global / buffer loads that write LDS directly) and the waits around it
+// ---------------------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+
+// This wave's vector-memory operations older than the newest N have completed (LDS-DMA
+// transfers included). expcnt / lgkmcnt are left at their maxima (no wait).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  // vmcnt(N) (bits 3:0 and 15:14)
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// Barrier for the DMA pipelines: this wave's DMA transfers older than the newest N have landed
+// and its own LDS reads have returned, then s_barrier. No memory-model fence: a workgroup release
+// fence would also wait for the newest DMA transfers (they write LDS), collapsing the pipeline to
+// one tile in flight. The signal fences keep the compiler from moving memory accesses across.
+template <int N>
+__device__ __forceinline__ void dma_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  // vmcnt(N), lgkmcnt(0), expcnt untouched
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4));
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 

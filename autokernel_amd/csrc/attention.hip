@@ -301,6 +301,445 @@ __global__ __launch_bounds__(kFaThreads, 8 / kFaWaves) void fa_fwd(
   }
 }
 
+// ============================================================================================
+// fa_fwd2: the main forward kernel (positive scale; one head's K / V rows addressable with
+// 32-bit byte offsets). Same work split and arithmetic as fa_fwd, built for gfx950's pipes:
+//   * K and V tiles reach LDS by LDS DMA (buffer_load_dwordx4 ... lds): no staging registers, no
+//     ds_write. The buffer resource of each tile ends at the last valid key, so rows past Sk
+//     arrive as zeros (their scores are masked; zero V rows add nothing).
+//   * V stays in its natural [key][d] layout. The V^T fragments of O^T += V^T P^T are read with
+//     ds_read_b64_tr_b16, which transposes a 4 x 16 block of 16-bit values across each group of
+//     16 lanes: output lane i, element e = element (i % 4) of source lane (i / 4 + 4 e). So source
+//     lane j of a group addresses V[key0 + j / 4][d0 + 4 (j % 4)] and output lane i receives
+//     V[key0 + e][d0 + i], e = 0..3: four consecutive keys of one d, as the MFMA's A operand needs.
+//   * Software pipeline per wave, one tile per iteration j:
+//       phase 1: O^T += V_{j-1}^T P_{j-1}^T (MFMA)   with   row max of S_j (VALU)
+//       phase 2: S_{j+1} = K_{j+1} Q^T (MFMA)        with   P_j = exp2(S_j - m), row sums (VALU)
+//     so every MFMA burst has independent softmax work beside it. Two barriers per tile (after
+//     each phase); each tile's DMA is issued 1.5 iterations before it is read.
+//   * Scores stay in raw units (Q K^T); the scale is folded into the exp2 argument. The
+//     reference's f16 overflow of Q K^T (or of its scaled value) turns a row into NaN exactly when
+//     some unmasked score reaches the overflow threshold (an inf score) or when every unmasked
+//     score is at or below minus the threshold (a row of -inf); both are decided once per row from
+//     the true row max.
+//   * Row sums add the rounded P values (v_dot2 with ones), so the weights that multiply V are
+//     the ones that are normalised.
+// LDS swizzles (16-byte chunk c of row r):
+//   K: c ^ (r & 15) for D = 128, c ^ ((r >> 1) & 7) for D = 64. gfx950 serves a ds_read_b128 in
+//      16-lane phases (256 bytes); the 16 lanes of a phase read rows r..r+15 at one chunk.
+//   V: c ^ (4 (r & 3) + 2 ((r >> 2) & 1)) for D = 128 (256-byte rows), c ^ (4 ((r >> 1) & 1) +
+//      2 ((r >> 2) & 1)) for D = 64 (128-byte rows). A tr read's 16-lane groups cover rows r..r+3
+//      (groups 0, 1) or r+4..r+7 (groups 2, 3) at 32 bytes each; any two of its groups land on
+//      distinct banks.
+// ============================================================================================
+template <int D>
+__device__ __forceinline__ int fa2_kswz(int r) {
+  if constexpr (D == 128) return r & 15;
+  else return (r >> 1) & 7;
+}
+template <int D>
+__device__ __forceinline__ int fa2_vswz(int r) {
+  if constexpr (D == 128) return 4 * (r & 3) + 2 * ((r >> 2) & 1);
+  else return 4 * ((r >> 1) & 1) + 2 * ((r >> 2) & 1);
+}
+
+// Raw buffer resource: loads at byte offsets >= nbytes return zeros.
+__device__ __forceinline__ u32x4 fa2_rsrc(const void* base, uint32_t nbytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  u32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);  // stride 0
+  r[2] = __builtin_amdgcn_readfirstlane(nbytes);
+  r[3] = 0x00020000u;  // 32-bit data format, untyped access
+  return r;
+}
+
+// One 1 KB LDS-DMA transfer: lane L's 16 bytes from rsrc + voff land at LDS byte lds + 16 L.
+// Inline assembly, so the compiler inserts no waits for it: every wait is an explicit vmcnt.
+__device__ __forceinline__ void fa2_dma16(const u32x4& rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %0, %1, 0 offen lds"
+      :
+      : "v"(voff), "s"(rsrc), "s"(lds)
+      : "memory", "m0");
+}
+
+typedef short fa2_s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 fa2_tr16(const uint16_t* p) {
+  return __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) fa2_s16x4*)(p)));
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t fa2_pack(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t fa2_pack<TF16>(float a, float b) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, f16x2));
+}
+template <>
+__device__ __forceinline__ uint32_t fa2_pack<TBF16>(float a, float b) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, b2));
+}
+// acc + p.lo + p.hi (p: two packed values)
+template <typename T>
+__device__ __forceinline__ float fa2_sum2(uint32_t p, float acc);
+template <>
+__device__ __forceinline__ float fa2_sum2<TF16>(uint32_t p, float acc) {
+  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p), one, acc, false);
+}
+template <>
+__device__ __forceinline__ float fa2_sum2<TBF16>(uint32_t p, float acc) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const b2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, p), one, acc, false);
+}
+
+// max over the two 32-lane halves (every lane gets the same value, combined in the same order)
+__device__ __forceinline__ float fa2_halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float fa2_halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kFaThreads, 2) void fa_fwd2(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    uint16_t* __restrict__ O, int Hq, int group, int Sq, int Sk, int64_t qsb, int64_t qsh,
+    int64_t qss, int64_t ksb, int64_t ksh, int kss, int64_t vsb, int64_t vsh, int vss,
+    int64_t osb, int64_t osh, int64_t oss, int causal, float c_log2, float thr, int nbh) {
+  static_assert(kFaWaves == 4 && kFaBKV == 64, "fa_fwd2 tiling");
+  constexpr int DC = D / 8;             // 16-byte chunks per row
+  constexpr int RPI = 64 / DC;          // rows per 1 KB DMA transfer
+  constexpr int NIW = kFaBKV / RPI / kFaWaves;  // transfers per wave per tile, per matrix
+  constexpr int NS = D / 16;            // 16-deep d steps of S^T
+  constexpr int NDB = D / 32;           // 32-row d blocks of O^T
+  constexpr int TILE = kFaBKV * D;      // elements of one K or V tile
+  static_assert(NIW * RPI * kFaWaves == kFaBKV, "tile rows split over waves");
+  __shared__ __attribute__((aligned(1024))) uint16_t sK[2 * TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t sV[2 * TILE];
+
+  const int bh = (int)(blockIdx.x % (unsigned)nbh);
+  const int qi = (int)(blockIdx.x / (unsigned)nbh);
+  const int nqb = (Sq + kFaBQ - 1) / kFaBQ;
+  const int qb = causal ? (nqb - 1 - qi) : qi;
+  const int h = bh % Hq, b = bh / Hq;
+  const int hk = h / group;
+  const int lane = lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int l32 = lane & 31, hh = lane >> 5;
+  const int q0 = qb * kFaBQ;
+  const int qw0 = q0 + w * 32;
+  const int my_q = qw0 + l32;
+
+  const uint16_t* Qb = Q + b * qsb + h * qsh;
+  const uint16_t* Kb = K + b * ksb + hk * ksh;
+  const uint16_t* Vb = V + b * vsb + hk * vsh;
+  uint16_t* Ob = O + b * osb + h * osh;
+
+  // Q fragments (B operand of S^T): lane holds query l32, d = s * 16 + hh * 8 .. + 8
+  u32x4 qf[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    qf[s] = (my_q < Sq) ? ld16(Qb + (int64_t)my_q * qss + s * 16 + hh * 8) : u32x4{0u, 0u, 0u, 0u};
+
+  const int kend = causal ? min(Sk, q0 + kFaBQ) : Sk;
+  const int nt = (kend + kFaBKV - 1) / kFaBKV;           // >= 1
+  const int jw = causal ? min(nt - 1, (qw0 + 31) / kFaBKV) : nt - 1;  // this wave's last tile
+
+  // Per-lane byte offsets of the DMA transfers inside a tile (the tile base is in the resource):
+  // transfer n = i * 4 + w covers tile rows n * RPI ..; lane L writes physical chunk L % DC of row
+  // n * RPI + L / DC and so fetches the logical chunk the swizzle maps there (XOR: its own inverse).
+  uint32_t offk[NIW], offv[NIW];
+#pragma unroll
+  for (int i = 0; i < NIW; ++i) {
+    const int row = (i * kFaWaves + w) * RPI + lane / DC;
+    const int pc = lane % DC;
+    offk[i] = (uint32_t)(row * kss * 2 + ((pc ^ fa2_kswz<D>(row)) * 16));
+    offv[i] = (uint32_t)(row * vss * 2 + ((pc ^ fa2_vswz<D>(row)) * 16));
+  }
+  const uint32_t sK_lds = (uint32_t)(uintptr_t)(lds_void*)sK;
+  const uint32_t sV_lds = (uint32_t)(uintptr_t)(lds_void*)sV;
+
+  auto issue_k = [&](int j, int stage) {
+    const int k0 = j * kFaBKV;
+    const u32x4 rs = fa2_rsrc(Kb + (int64_t)k0 * kss, (uint32_t)(((Sk - 1 - k0) * kss + D) * 2));
+#pragma unroll
+    for (int i = 0; i < NIW; ++i) fa2_dma16(rs, offk[i], sK_lds + stage * TILE * 2 + (i * kFaWaves + w) * 1024);
+  };
+  auto issue_v = [&](int j, int stage) {
+    const int k0 = j * kFaBKV;
+    const u32x4 rs = fa2_rsrc(Vb + (int64_t)k0 * vss, (uint32_t)(((Sk - 1 - k0) * vss + D) * 2));
+#pragma unroll
+    for (int i = 0; i < NIW; ++i) fa2_dma16(rs, offv[i], sV_lds + stage * TILE * 2 + (i * kFaWaves + w) * 1024);
+  };
+
+  // S^T = K Q^T for the 64 keys of a tile: two 32-key accumulators, issued alternately
+  auto qk = [&](const uint16_t* ks, f32x16 (&s)[2]) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) s[kb][v] = 0.f;
+#pragma unroll
+    for (int st = 0; st < NS; ++st)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int r = kb * 32 + l32;
+        const int c = st * 2 + hh;
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(&ks[r * D + (c ^ fa2_kswz<D>(r)) * 8]);
+        s[kb] = mfma32x32x16<T>(kf, qf[st], s[kb]);
+      }
+  };
+
+  // O^T += V^T P^T over the 64 keys of a tile: 16-key step t, lane-half hh carries keys
+  // 16 t + 4 hh + 0..3 and 16 t + 8 + 4 hh + 0..3 (the S^T accumulator order, see softmax below).
+  f32x16 o[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[i][v] = 0.f;
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const int vrow = 4 * (g16 >> 1) + (i16 >> 2);          // + 16 t (+ 8 for the second read)
+  const int vcol = 16 * (g16 & 1) + 4 * (i16 & 3);       // + 32 db
+  const int vsw = fa2_vswz<D>(vrow);                      // same for rows + 8, + 16 t
+  u32x4 pf[4];
+  auto pv = [&](const uint16_t* vs) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const int col = db * 32 + vcol;
+        const uint16_t* p = vs + (16 * t + vrow) * D + (((col >> 3) ^ vsw) * 8) + (col & 7);
+        const u32x2 lo = fa2_tr16(p);
+        const u32x2 hi = fa2_tr16(p + 8 * D);
+        const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
+        o[db] = mfma32x32x16<T>(vf, pf[t], o[db]);
+      }
+  };
+
+  float m_run = -INFINITY, l_run = 0.f, m_true = -INFINITY;
+  // row statistics of S_j: mask, tile max (raw units), lazy base update
+  auto stats = [&](f32x16 (&s)[2], int k0, bool masked, float& alpha, float& base) {
+    if (masked) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = k0 + kb * 32 + (v >> 2) * 8 + hh * 4 + (v & 3);
+          if (key >= Sk || (causal && key > my_q)) s[kb][v] = -INFINITY;
+        }
+    }
+    // four independent max3 chains over the 32 scores, then one combine
+    float m4[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int kb = c >> 1, v0 = (c & 1) * 8;
+      float m = fmaxf(fmaxf(s[kb][v0], s[kb][v0 + 1]), s[kb][v0 + 2]);
+      m = fmaxf(fmaxf(m, s[kb][v0 + 3]), s[kb][v0 + 4]);
+      m = fmaxf(fmaxf(m, s[kb][v0 + 5]), s[kb][v0 + 6]);
+      m4[c] = fmaxf(m, s[kb][v0 + 7]);
+    }
+    float mt = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+    mt = fa2_halves_max(mt);
+    m_true = fmaxf(m_true, mt);
+    const float mts = mt * c_log2;
+    const float m_new = (mts > m_run + kFaRescaleSlack || m_run == -INFINITY) ? fmaxf(m_run, mts) : m_run;
+    base = (m_new == -INFINITY) ? 0.f : m_new;
+    alpha = (m_new == m_run) ? 1.0f : __builtin_amdgcn_exp2f(m_run - base);
+    m_run = m_new;
+  };
+  // Exponent arguments in place: S_j * c - base (log2 units).
+  auto exp_args = [&](f32x16 (&s)[2], float base) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) s[kb][v] = __builtin_fmaf(s[kb][v], c_log2, -base);
+  };
+  // P_j = exp2(argument), rounded to the element type and packed as the B operand of the O^T
+  // update; returns the row-half sum of the rounded values.
+  auto exp_pack = [&](const f32x16 (&s)[2]) -> float {
+    float ps = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int v = 8 * (t & 1) + 2 * e;
+        const float x0 = __builtin_amdgcn_exp2f(s[t >> 1][v]);
+        const float x1 = __builtin_amdgcn_exp2f(s[t >> 1][v + 1]);
+        const uint32_t pk = fa2_pack<T>(x0, x1);
+        pf[t][e] = pk;
+        ps = fa2_sum2<T>(pk, ps);
+      }
+    return ps;
+  };
+
+  // end of iteration j: every wave is done with V_{j-1} and K_{j+1}, and V_j and K_{j+2} (issued
+  // one iteration ago) have landed; refill the two free stages.
+  // DMA schedule (two LDS stages each for K and V; tile t lives in stage t & 1):
+  //   mid(j), after phase 1 of iteration j: every wave is done with V_{j-1}; V_{j+1} goes into its
+  //     stage. K_{j+1}, read in phase 2, must have landed.
+  //   end(j), after phase 2: every wave is done with K_{j+1}; K_{j+3} goes into its stage. V_j,
+  //     read in phase 1 of iteration j + 1, must have landed.
+  // Each transfer so has 1.5 iterations to land. vmcnt retires transfers in issue order, so a
+  // wait lets exactly the transfers issued after the needed one stay in flight (two groups of
+  // NIW in the steady state, fewer near the end).
+  auto barrier_after = [&](int later) {
+    if (later >= 2) dma_barrier<2 * NIW>();
+    else if (later == 1) dma_barrier<NIW>();
+    else dma_barrier<0>();
+  };
+  auto sync_mid = [&](int j, int par) {
+    // issued after K_{j+1}: V_j (mid j-1; in the prologue for j = 0, waited there) and K_{j+2}
+    barrier_after(j == 0 ? 0 : 1 + (j + 2 < nt));
+    if (j + 1 < nt) issue_v(j + 1, par ^ 1);
+  };
+  auto sync_end = [&](int j, int par) {
+    // issued after V_j: K_{j+2} (end j-1) and V_{j+1} (mid j); V_0 was waited in the prologue
+    barrier_after(j == 0 ? 0 : (j + 2 < nt) + (j + 1 < nt));
+    if (j + 3 < nt) issue_k(j + 3, par ^ 1);
+  };
+  f32x16 sa[2], sb[2];
+  // General iteration j (parity par = j & 1): S holds S_j, Sn receives S_{j+1}. Each phase runs
+  // only where this wave needs it (causal tail, first tile), and diagonal / partial tiles are
+  // masked.
+  auto iter = [&](int j, int par, f32x16 (&S)[2], f32x16 (&Sn)[2]) {
+    const int k0 = j * kFaBKV;
+    if (j > 0 && j - 1 <= jw) pv(sV + (par ^ 1) * TILE);  // V_{j-1}
+    float alpha = 1.0f, base = 0.f;
+    const bool act = j <= jw;
+    if (act) {
+      const bool masked = (causal && k0 + kFaBKV - 1 > qw0) || (k0 + kFaBKV > Sk);
+      stats(S, k0, masked, alpha, base);
+    }
+    sync_mid(j, par);
+    if (j + 1 <= jw) qk(sK + (par ^ 1) * TILE, Sn);  // K_{j+1}
+    if (act) {
+      exp_args(S, base);
+      const float ps = exp_pack(S);
+      l_run = l_run * alpha + ps;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+        for (int i = 0; i < NDB; ++i)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) o[i][v] *= alpha;
+      }
+    }
+    sync_end(j, par);
+  };
+  // Steady-state iteration (1 <= j, tile j unmasked, j + 1 <= jw): all four parts run, with no
+  // branch between them, so the MFMAs of one part and the VALU work of the other share one block.
+  auto iter_fast = [&](int j, int par, f32x16 (&S)[2], f32x16 (&Sn)[2]) {
+    // phase 1: O^T += V_{j-1}^T P_{j-1}^T beside the row max of S_j and its exponent arguments.
+    // Fragment reads run two MFMAs ahead of their use.
+    pv(sV + (par ^ 1) * TILE);
+    float alpha, base;
+    stats(S, j * kFaBKV, false, alpha, base);
+    exp_args(S, base);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 14; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the V^T fragment of MFMA i + 2
+      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // 5 VALU
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    sync_mid(j, par);
+    // phase 2: S_{j+1} = K_{j+1} Q^T beside P_j = exp2(...) and its row sum
+    qk(sK + (par ^ 1) * TILE, Sn);
+    const float ps = exp_pack(S);
+    // keep P_j's computation here (otherwise it sinks to its first use after the barrier)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) asm volatile("" ::"v"(pf[t]));
+    asm volatile("" ::"v"(ps));
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+#pragma unroll
+    for (int i = 0; i < 14; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);  // the K fragment of MFMA i + 2
+      __builtin_amdgcn_sched_group_barrier(0x402, 4, 1);  // 4 VALU / transcendental
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x402, 4, 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    l_run = l_run * alpha + ps;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+      for (int i = 0; i < NDB; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[i][v] *= alpha;
+    }
+    sync_end(j, par);
+  };
+
+  issue_k(0, 0);
+  if (nt > 1) issue_k(1, 1);
+  issue_v(0, 0);
+  dma_barrier<0>();
+  qk(sK, sa);  // S_0 (jw >= 0 always)
+  dma_barrier<0>();
+  if (nt > 2) issue_k(2, 0);
+  // first masked tile of this wave (diagonal or partial), and the end of the steady range
+  const int jm_s = Sk / kFaBKV;
+  const int jm = causal ? min((qw0 + 1) / kFaBKV, jm_s) : jm_s;
+  const int jf = max(1, min(jm, jw));
+  // Register roles are fixed at compile time: S_j is in sb at odd j of the steady loop, in sa
+  // at even j; the general iterations always take S_j from sa and leave S_{j+1} in sa.
+  iter(0, 0, sa, sb);
+  int j = 1;
+  for (; j + 1 < jf; j += 2) {
+    iter_fast(j, 1, sb, sa);
+    iter_fast(j + 1, 0, sa, sb);
+  }
+  if (j < jf) {
+    iter_fast(j, 1, sb, sa);
+    ++j;
+  } else {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) sa[kb] = sb[kb];
+  }
+  for (; j < nt; ++j) {
+    iter(j, j & 1, sa, sb);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) sa[kb] = sb[kb];
+  }
+  if (nt - 1 <= jw) pv(sV + ((nt - 1) & 1) * TILE);
+  wait_vmcnt<0>();  // (no transfer is outstanding here; kept so none can outlive the block)
+
+  // ---- epilogue: O[q][d] = O^T[d][q] / l; NaN rows where the reference's scores overflow ----
+  const float l_tot = fa2_halves_sum(l_run);
+  const bool nan_row = !(m_true < thr && m_true > -thr);
+  const float inv = nan_row ? __builtin_nanf("") : 1.0f / l_tot;
+  if (my_q < Sq) {
+    uint16_t* orow = Ob + (int64_t)my_q * oss;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = db * 32 + g * 8 + hh * 4;
+        u32x2 pk;
+        pk[0] = fa2_pack<T>(o[db][g * 4 + 0] * inv, o[db][g * 4 + 1] * inv);
+        pk[1] = fa2_pack<T>(o[db][g * 4 + 2] * inv, o[db][g * 4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + d) = pk;
+      }
+  }
+}
+
 template <typename T, int D>
 static int launch_fa(const void* Q, const void* K, const void* V, void* O, int64_t B, int64_t Hq,
                      int64_t Hkv, int64_t Sq, int64_t Sk, const int64_t* qs, const int64_t* ks,
@@ -310,6 +749,17 @@ static int launch_fa(const void* Q, const void* K, const void* V, void* O, int64
   const dim3 grid((unsigned)nblocks);
   // Scores whose f16 rounding (or f16 scaling by sm_scale) overflows become +-inf.
   const float thr = 65520.0f / fmaxf(1.0f, fabsf(sm_scale));
+  // fa_fwd2 folds a positive scale into exp2 and addresses one head's K / V rows with 32-bit
+  // byte offsets; anything else takes fa_fwd.
+  const int64_t span = (int64_t)2 * Sk * (ks[2] > vs[2] ? ks[2] : vs[2]);
+  if (sm_scale > 0.f && span < ((int64_t)1 << 31) && ks[2] >= D && vs[2] >= D) {
+    fa_fwd2<T, D><<<grid, kFaThreads, 0, st>>>(
+        (const uint16_t*)Q, (const uint16_t*)K, (const uint16_t*)V, (uint16_t*)O, (int)Hq,
+        (int)(Hq / Hkv), (int)Sq, (int)Sk, qs[0], qs[1], qs[2], ks[0], ks[1], (int)ks[2], vs[0],
+        vs[1], (int)vs[2], os[0], os[1], os[2], causal, sm_scale * kFaLog2e,
+        T::kCode == AK_F16 ? thr : INFINITY, (int)(Hq * B));
+    return record_launch();
+  }
   fa_fwd<T, D><<<grid, kFaThreads, 0, st>>>(
       (const uint16_t*)Q, (const uint16_t*)K, (const uint16_t*)V, (uint16_t*)O, (int)Hq,
       (int)(Hq / Hkv), (int)Sq, (int)Sk, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1],

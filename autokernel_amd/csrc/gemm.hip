@@ -304,14 +304,7 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma(
 // in 8 distinct 16-byte bank slots (measured for 128-byte rows: SQ_LDS_BANK_CONFLICT 0 with
 // chunk c ^ (row & 7), 50% with an extra row-bit-3 term, 75% unswizzled).
 // --------------------------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Barrier for the DMA pipelines: this wave's DMA transfers older than the newest N have landed
-// and its own LDS reads have returned, then s_barrier. No memory-model fence: a workgroup release
-// fence would also wait for the newest DMA transfers (they write LDS), collapsing the pipeline to
-// one tile in flight. The signal fences keep the compiler from moving memory accesses across.
-template <int N>
-__device__ __forceinline__ void dma_barrier();
+// LDS-DMA helpers (lds_void, wait_vmcnt, dma_barrier) live in ak_common.h.
 
 // The same transfer as inline assembly. The compiler then does not track it: its wait-count pass
 // inserts no waits for it (a conservative full wait at a loop head otherwise drains the whole
@@ -326,23 +319,6 @@ __device__ __forceinline__ void dma16_asm(const char* base, uint32_t off, uint16
       :
       : "v"(off), "s"(base), "s"(lds)
       : "memory", "m0");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt field");
-  // vmcnt(N) (bits 3:0 and 15:14), expcnt / lgkmcnt at their maxima (no wait)
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-}
-
-template <int N>
-__device__ __forceinline__ void dma_barrier() {
-  static_assert(N >= 0 && N < 64, "vmcnt field");
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  // vmcnt(N), lgkmcnt(0), expcnt untouched
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4));
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // Multi-stage variant: NS LDS stages of BKD-deep tiles (BKD 64: 128-byte rows, chunk c of row r
