@@ -339,17 +339,41 @@ struct DmaGeom<32> {
   __device__ static __forceinline__ int swz(int r, int c) { return c ^ ((r >> 2) & 1); }
 };
 
-template <typename T, int BM, int BN, int WM, int WN, int NB, int BKD, int NS>
+// [K, N] B (N contiguous, torch.matmul's B) is staged as [k][n] tile rows. The MFMA operand needs
+// 8 consecutive k of one n per lane: two ds_read_b64_tr_b16 each give 4. That instruction
+// transposes across each group of 16 lanes: output lane i, element e = element (i % 4) of source
+// lane (i / 4 + 4 e); so source lane j addresses B[k0 + j / 4][n0 + 4 (j % 4)] and output lane i
+// receives B[k0 + e][n0 + i]. 16-byte chunk c of tile row k is stored at c ^ bkn_swz(k): the 16
+// rows of one tr read (4 per lane group) land on distinct banks for lane groups {0,1}, {2,3},
+// {0,2} and {1,3}.
+__device__ __forceinline__ int bkn_swz(int k) { return 2 * ((k & 3) + 4 * (((k >> 3) ^ (k >> 4)) & 1)); }
+
+typedef short gemm_s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 lds_tr16(const uint16_t* p) {
+  return __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) gemm_s16x4*)(p)));
+}
+
+// B-side DMA geometry: BKN (B is [K, N]) stages BKD rows of BN elements, else BN rows of BKD.
+template <int BN, int BKD, bool BKN>
+struct DmaB {
+  static constexpr int kRowElems = BKN ? BN : BKD;
+  static constexpr int RPI = 512 / kRowElems;    // tile rows per 1 KB transfer
+  static constexpr int kRows = BKN ? BKD : BN;   // tile rows per stage
+};
+
+template <typename T, int BM, int BN, int WM, int WN, int NB, int BKD, int NS, bool BKN>
 __device__ __forceinline__ void gemm_dma_ns_kloop(
     f32x4 (&acc)[NB][BM / WM / 16][BN / WN / 16], const uint16_t* A, const uint16_t* B0,
-    const uint16_t* B1, const uint32_t* oa, const uint32_t* ob, int K, int wid, int wm, int wn,
-    int lane, uint16_t* s0, uint16_t* s1, uint16_t* s2, uint16_t* s3) {
+    const uint16_t* B1, const uint32_t* oa, const uint32_t* ob, uint32_t kb_step_b, int K, int wid,
+    int wm, int wn, int lane, uint16_t* s0, uint16_t* s1, uint16_t* s2, uint16_t* s3) {
   using G = DmaGeom<BKD>;
+  using GB = DmaB<BN, BKD, BKN>;
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
   constexpr int A_INS = BM / G::RPI / NW;
-  constexpr int B_INS = BN / G::RPI / NW;
+  constexpr int B_INS = GB::kRows / GB::RPI / NW;
   constexpr int INS = A_INS + NB * B_INS;
   constexpr int H = FM / 2;
   constexpr int STEPS = BKD / 32;  // k-steps of 32 per tile
@@ -360,15 +384,15 @@ __device__ __forceinline__ void gemm_dma_ns_kloop(
 
   auto issue = [&](int kt, uint16_t* sp) {
     const uint32_t kb = 2u * (uint32_t)(kt * BKD);
+    const uint32_t kbb = BKN ? (uint32_t)kt * kb_step_b : kb;
 #pragma unroll
     for (int i = 0; i < A_INS; ++i)
-      dma16_asm(reinterpret_cast<const char*>(A), oa[i] + kb, sp + (i * NW + wid) * G::RPI * BKD);
+      dma16_asm(reinterpret_cast<const char*>(A), oa[i] + kb, sp + (i * NW + wid) * 512);
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int i = 0; i < B_INS; ++i)
-        dma16_asm(reinterpret_cast<const char*>(Bm[b]), ob[i] + kb,
-                  sp + (BM + b * BN) * BKD + (i * NW + wid) * G::RPI * BKD);
+        dma16_asm(reinterpret_cast<const char*>(Bm[b]), ob[i] + kbb, sp + (BM + b * BN) * BKD + (i * NW + wid) * 512);
   };
   u32x4 fa[FM], fb[NB][FN], fbn[NB][FN];
   auto frag = [&](const uint16_t* base, int row, int s) -> u32x4 {
@@ -382,7 +406,20 @@ __device__ __forceinline__ void gemm_dma_ns_kloop(
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) dst[b][j] = frag(sp + (BM + b * BN) * BKD, wn * WTN + j * 16 + fr, s);
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (BKN) {
+          // k = 32 s + 8 (lane / 16) + 0..3 and + 4..7 for n = wn * WTN + 16 j + lane % 16
+          const uint16_t* bs = sp + (BM + b * BN) * BKD;
+          const int row = s * 32 + 8 * fc + (fr >> 2);
+          const int col = wn * WTN + j * 16 + 4 * (fr & 3);
+          const uint16_t* p = bs + row * BN + (((col >> 3) ^ bkn_swz(row)) * 8) + (col & 7);
+          const u32x2 lo = lds_tr16(p);
+          const u32x2 hi = lds_tr16(p + 4 * BN);  // rows + 4 share the swizzle
+          dst[b][j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        } else {
+          dst[b][j] = frag(sp + (BM + b * BN) * BKD, wn * WTN + j * 16 + fr, s);
+        }
+      }
   };
   auto mfma_rows = [&](int i0, int i1) {
 #pragma unroll
@@ -437,7 +474,7 @@ __device__ __forceinline__ void gemm_dma_ns_kloop(
   wait_vmcnt<0>();  // no DMA may still target this block's LDS when its waves end
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, int BKD, int NS>
+template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, int BKD, int NS, bool BKN>
 __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B0, const uint16_t* __restrict__ B1,
     uint16_t* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
@@ -446,9 +483,10 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
   constexpr int RPI = DmaGeom<BKD>::RPI;  // tile rows per DMA instruction (1 KB)
+  using GB = DmaB<BN, BKD, BKN>;
   constexpr int A_INS = BM / RPI / NW;  // DMA instructions per wave per tile for A
-  constexpr int B_INS = BN / RPI / NW;  // ... per B matrix
-  static_assert(A_INS * RPI * NW == BM && B_INS * RPI * NW == BN, "tile rows split over waves");
+  constexpr int B_INS = GB::kRows / GB::RPI / NW;  // ... per B matrix
+  static_assert(A_INS * RPI * NW == BM && B_INS * GB::RPI * NW == GB::kRows, "tile rows split over waves");
   static_assert(4 * (A_INS + NB * B_INS) < 64, "outstanding DMA fits vmcnt");
   static_assert(FM % 2 == 0, "two MFMA halves per k-step");
   constexpr int kStage = (BM + NB * BN) * BKD;  // elements per stage
@@ -478,10 +516,20 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
   uint32_t ob[B_INS];
 #pragma unroll
   for (int i = 0; i < B_INS; ++i) {
-    const int row = (i * NW + wid) * RPI + r_in;
-    const int lc = DmaGeom<BKD>::swz(row, pc);
-    ob[i] = 2u * (uint32_t)(min(n0 + row, N - 1) * (int)ldb + lc * 8);
+    if constexpr (BKN) {
+      // tile row = k (relative to the tile's first k), BN / 8 chunks per row; columns past N are
+      // clamped onto the last full chunk (their results are never stored)
+      constexpr int CPR = BN / 8;
+      const int row = (i * NW + wid) * GB::RPI + lane / CPR;
+      const int lc = (lane % CPR) ^ bkn_swz(row);
+      ob[i] = 2u * (uint32_t)(row * (int)ldb + min(n0 + lc * 8, N - 8));
+    } else {
+      const int row = (i * NW + wid) * RPI + r_in;
+      const int lc = DmaGeom<BKD>::swz(row, pc);
+      ob[i] = 2u * (uint32_t)(min(n0 + row, N - 1) * (int)ldb + lc * 8);
+    }
   }
+  const uint32_t kb_step_b = 2u * (uint32_t)BKD * (uint32_t)ldb;  // B bytes per k-tile ([K, N] B)
 
   f32x4 acc[NB][FM][FN];
 #pragma unroll
@@ -491,8 +539,8 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[b][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  gemm_dma_ns_kloop<T, BM, BN, WM, WN, NB, BKD, NS>(acc, A, B0, B1, oa, ob, K, wid, wm, wn, lane, sS0, sS1, sS2,
-                                                    sS3);
+  gemm_dma_ns_kloop<T, BM, BN, WM, WN, NB, BKD, NS, BKN>(acc, A, B0, B1, oa, ob, kb_step_b, K, wid, wm, wn, lane,
+                                                         sS0, sS1, sS2, sS3);
 
   const int fr = lane & 15, fc = lane >> 4;
 #pragma unroll
@@ -722,10 +770,10 @@ constexpr bool kUseDma = AK_GEMM_DMA != 0;
 constexpr bool kUseDeep = AK_GEMM_DEEP != 0;
 constexpr int kCUs = 256;  // MI355X compute units
 
-template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, int BKD, int NS>
+template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, int BKD, int NS, bool BKN>
 static void launch_dma_kernel(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
                               int64_t lda, int64_t ldb, int64_t ldc, int tiles_m, int tiles_n, hipStream_t s) {
-  gemm_dma<T, BM, BN, WM, WN, NB, EPI, BKD, NS><<<tiles_m * tiles_n, WM * WN * kWave, 0, s>>>(
+  gemm_dma<T, BM, BN, WM, WN, NB, EPI, BKD, NS, BKN><<<tiles_m * tiles_n, WM * WN * kWave, 0, s>>>(
       (const uint16_t*)A, (const uint16_t*)B0, (const uint16_t*)B1, (uint16_t*)C, M, N, K, lda, ldb, ldc,
       tiles_m, tiles_n);
 }
@@ -750,7 +798,7 @@ struct DmaPlan {
                             : (kOk32 ? 4 : 2);
 };
 
-template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI>
+template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, bool BKN>
 static void launch_dma_cfg(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
                            int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
   const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(N, BN);
@@ -760,25 +808,29 @@ static void launch_dma_cfg(const void* A, const void* B0, const void* B1, void* 
   constexpr bool kOk32 = P::kOk32;
   if (kOk32 && kUseDeep && tiles_m * tiles_n < kCUs) {
     if constexpr (kOk32)
-      launch_dma_kernel<T, BM, BN, WM, WN, NB, EPI, 32, 4>(A, B0, B1, C, M, N, K, lda, ldb, ldc, tiles_m, tiles_n, s);
+      launch_dma_kernel<T, BM, BN, WM, WN, NB, EPI, 32, 4, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, tiles_m,
+                                                                tiles_n, s);
     return;
   }
-  launch_dma_kernel<T, BM, BN, WM, WN, NB, EPI, P::BKD, P::NS>(A, B0, B1, C, M, N, K, lda, ldb, ldc, tiles_m,
-                                                               tiles_n, s);
+  launch_dma_kernel<T, BM, BN, WM, WN, NB, EPI, P::BKD, P::NS, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, tiles_m,
+                                                                    tiles_n, s);
 }
 
-template <typename T, int NB, int EPI>
+template <typename T, int NB, int EPI, bool BKN>
 static void launch_gemm_dma(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
                             int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
   const TileCfg t = pick_tile(M, N, NB);
   if constexpr (NB == 1) {
-    if (t.bm == 256 && t.bn == 256) launch_dma_cfg<T, 256, 256, 2, kBigWN, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
-    else if (t.bm == 256) launch_dma_cfg<T, 256, 128, 4, 2, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
-    else launch_dma_cfg<T, 128, 128, 2, 2, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+    if (t.bm == 256 && t.bn == 256)
+      launch_dma_cfg<T, 256, 256, 2, kBigWN, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+    else if (t.bm == 256) launch_dma_cfg<T, 256, 128, 4, 2, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+    else launch_dma_cfg<T, 128, 128, 2, 2, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
   } else {
-    if (t.bm == 256 && t.bn == 256) launch_dma_cfg<T, 256, 128, 2, kBigWN, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
-    else if (t.bm == 256) launch_dma_cfg<T, 256, 64, 4, 2, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
-    else launch_dma_cfg<T, 128, 64, 2, 2, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+    static_assert(!BKN, "gate/up weights are [H, D]");
+    if (t.bm == 256 && t.bn == 256)
+      launch_dma_cfg<T, 256, 128, 2, kBigWN, 2, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+    else if (t.bm == 256) launch_dma_cfg<T, 256, 64, 4, 2, 2, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+    else launch_dma_cfg<T, 128, 64, 2, 2, 2, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
   }
 }
 
@@ -793,8 +845,16 @@ static int launch_gemm16(const void* A, const void* B0, const void* B1, void* C,
   // LDS-DMA path: nn.Linear-layout B, K a multiple of 64, 32-bit element offsets
   const bool fits32 = M * lda < INT_MAX && N * ldb < INT_MAX;
   if (bt && vec && K % kBK == 0 && K > 0 && fits32 && kUseDma) {
-    launch_gemm_dma<T, NB, EPI>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s);
+    launch_gemm_dma<T, NB, EPI, false>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s);
     return record_launch();
+  }
+  // [K, N] B (torch.matmul's layout) on the same pipeline, fragments read through LDS transposes
+  if constexpr (NB == 1) {
+    const bool fits32_kn = M * lda < INT_MAX && K * ldb < INT_MAX;
+    if (!bt && vec && K % kBK == 0 && K > 0 && N >= 8 && fits32_kn && kUseDma) {
+      launch_gemm_dma<T, 1, EPI, true>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s);
+      return record_launch();
+    }
   }
   if (bt) {
     if (vec) launch_gemm_tiled<T, true, true, NB, EPI>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s);

@@ -3,7 +3,8 @@
 Mirrors reference.py:10-12 and kernels/matmul.py:62. A: [..., M, K] (leading dims flattened into
 M when B is 2-D), B: [K, N]; batched B loops over the batch. When B is a transposed view of a
 row-major [N, K] tensor (nn.Linear's weight.t()), the GEMM reads it in place (b_trans = 1)
-instead of copying. Runs ak_gemm (gemm.hip).
+instead of copying; a row-major [K, N] B is read in place too (b_trans = 0). Runs ak_gemm
+(gemm.hip).
 """
 from __future__ import annotations
 
@@ -24,12 +25,6 @@ def _b_layout(B: torch.Tensor) -> tuple[torch.Tensor, int, int]:
         return B, B.stride(1), 1
     Bc = B.contiguous()
     return Bc, max(N, 1), 0
-
-
-# [K, N] operands at least this large are transposed once (ak_transpose) and multiplied by the
-# K-contiguous LDS-DMA GEMM; the transpose moves 2*K*N elements, far less than the register
-# transpose inside the [K, N] GEMM kernel costs at these sizes.
-NN_TRANSPOSE_MIN_MNK = 256 * 256 * 256
 
 
 def transpose(B: torch.Tensor) -> torch.Tensor:
@@ -57,9 +52,6 @@ def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> t
         A = A.contiguous()
     lda = A.stride(0) if M > 1 else max(K, 1)
     Bt, ldb, bt = _b_layout(B)
-    if (bt == 0 and A.dtype != torch.float32 and K % 64 == 0 and K % 8 == 0 and
-            M * N * K >= NN_TRANSPOSE_MIN_MNK):
-        Bt, ldb, bt = transpose(Bt if Bt.stride(0) == ldb and Bt.stride(1) == 1 else Bt.contiguous()), K, 1
     C = out if out is not None else torch.empty((M, N), device=A.device, dtype=A.dtype)
     if K == 0:
         return C.zero_()
