@@ -480,7 +480,7 @@ static int launch_reduce(const void* x, void* y, int64_t outer, int64_t red_n, i
     RowPlan plan;
     const bool vec = cols % T::kVec == 0 && host_aligned16(x);
     bool handled = false;
-    if (vec && plan_row(cols / T::kVec, T::kVec, &plan)) {
+    if (vec && plan_row(cols / T::kVec, T::kVec, &plan, 2)) {
       AK_ROW_SWITCH({
         const dim3 grid((unsigned)cdiv(rows, RowGeom<L>::kRowsPerBlock));
         reduce_rows<T, L, VPT, MAX><<<grid, RowGeom<L>::kThreads, 0, s>>>(xp, yp, rows, (int)cols);
