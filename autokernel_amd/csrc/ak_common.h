@@ -93,28 +93,58 @@ __device__ __forceinline__ void st16_stream(void* p, const u32x4& v) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Wave64 butterfly reductions. The xor pattern fixes the combination order, so results are
-// bitwise reproducible run to run.
+// Wave64 reductions on the VALU. Steps 0-3 exchange inside rows of 16 lanes through DPP (lane ^ 1,
+// lane ^ 2, the mirrored lane of an 8-lane half row, the mirrored lane of a 16-lane row); steps 4
+// and 5 pair 16-lane rows through v_permlane16_swap and 32-lane halves through v_permlane32_swap.
+// After steps 0..k every lane of an aligned 2^(k+1)-lane segment holds the segment's result. Each
+// step combines two values with a commutative operation, so all lanes hold the same bits and the
+// order is the same run to run (bitwise reproducible).
 // ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+template <int STEP, typename Op>
+__device__ __forceinline__ float wave_step(float v, Op op) {
+  if constexpr (STEP < 4) {
+    // quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror
+    constexpr int ctrl = STEP == 0 ? 0xB1 : STEP == 1 ? 0x4E : STEP == 2 ? 0x141 : 0x140;
+    const float p = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
+    return op(v, p);
+  } else if constexpr (STEP == 4) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+}
+// Reduce over aligned segments of L lanes (L a power of two, 1..64); every lane gets its result.
+template <int L, typename Op>
+__device__ __forceinline__ float seg_reduce(float v, Op op) {
+  static_assert(L >= 1 && L <= 64 && (L & (L - 1)) == 0, "segment of 1..64 lanes");
+  if constexpr (L >= 2) v = wave_step<0>(v, op);
+  if constexpr (L >= 4) v = wave_step<1>(v, op);
+  if constexpr (L >= 8) v = wave_step<2>(v, op);
+  if constexpr (L >= 16) v = wave_step<3>(v, op);
+  if constexpr (L >= 32) v = wave_step<4>(v, op);
+  if constexpr (L >= 64) v = wave_step<5>(v, op);
   return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
-}
+
 // NaN-propagating max (torch.max semantics): any NaN operand gives NaN.
 __device__ __forceinline__ float nan_max(float a, float b) {
   return (a != a || a > b) ? a : b;
 }
-__device__ __forceinline__ float wave_nan_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = nan_max(v, __shfl_xor(v, o, kWave));
-  return v;
-}
+
+struct OpAdd {
+  __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+struct OpMax {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct OpNanMax {
+  __device__ __forceinline__ float operator()(float a, float b) const { return nan_max(a, b); }
+};
+__device__ __forceinline__ float wave_sum(float v) { return seg_reduce<kWave>(v, OpAdd()); }
+__device__ __forceinline__ float wave_max(float v) { return seg_reduce<kWave>(v, OpMax()); }
+__device__ __forceinline__ float wave_nan_max(float v) { return seg_reduce<kWave>(v, OpNanMax()); }
 
 // ---------------------------------------------------------------------------------------------
 // LDS DMA (global / buffer loads that write LDS directly) and the waits around it

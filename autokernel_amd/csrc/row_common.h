@@ -19,25 +19,14 @@ namespace ak {
 #endif
 constexpr bool kRowStream = AK_ROW_STREAM != 0;
 
-// Butterfly over the L lanes of a segment (L <= 64): every lane ends with the segment result.
+// Reduction over the L lanes of a segment (L <= 64: every lane ends with the segment result; a
+// wider group reduces each of its waves here and combines them in group_combine).
 template <int L>
-__device__ __forceinline__ float seg_sum(float v) {
-#pragma unroll
-  for (int o = (L < kWave ? L : kWave) / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
+__device__ __forceinline__ float seg_sum(float v) { return seg_reduce<(L < kWave ? L : kWave)>(v, OpAdd()); }
 template <int L>
-__device__ __forceinline__ float seg_max(float v) {
-#pragma unroll
-  for (int o = (L < kWave ? L : kWave) / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
-}
+__device__ __forceinline__ float seg_max(float v) { return seg_reduce<(L < kWave ? L : kWave)>(v, OpMax()); }
 template <int L>
-__device__ __forceinline__ float seg_nan_max(float v) {
-#pragma unroll
-  for (int o = (L < kWave ? L : kWave) / 2; o > 0; o >>= 1) v = nan_max(v, __shfl_xor(v, o, kWave));
-  return v;
-}
+__device__ __forceinline__ float seg_nan_max(float v) { return seg_reduce<(L < kWave ? L : kWave)>(v, OpNanMax()); }
 
 // Combine per-wave partials of a group of L > 64 lanes (L / 64 waves) through LDS.
 // Every wave of the block must call it (it contains barriers). kind: 0 sum, 1 max, 2 nan-max.
