@@ -75,9 +75,11 @@ def run() -> None:
 
 
 MFMA_PROBES = [  # kernel-name fragment, label, flops per launch
-    ("gemm_dma<ak::TBF16, 256, 256", "matmul bf16 4096^3 (NT, LDS-DMA)", 2 * 4096 ** 3),
-    ("gemm_dma<ak::TBF16, 256, 128, 2, 4, 2", "fused_mlp gate/up bf16 2048x4096 H=11008", 2 * 2048 * 4096 * 11008 * 2),
-    ("fa_fwd<ak::TF16, 128>", "flash_attention f16 causal [4,32,2048,128]", 2 * 2 * 4 * 32 * 128 * (2048 * 2049 // 2)),
+    ("gemm_dma<ak::TBF16, 256, 256, 2, 4, 1, 0, 64, 2, true>", "matmul bf16 4096^3 (NN: [K, N] B, LDS-DMA)",
+     2 * 4096 ** 3),
+    ("gemm_dma<ak::TBF16, 256, 128, 2, 4, 2, 1", "fused_mlp gate/up bf16 2048x4096 H=11008", 2 * 2048 * 4096 * 11008 * 2),
+    ("gemm_dma<ak::TBF16, 256, 128, 4, 2, 1, 0", "fused_mlp down bf16 2048x4096 K=11008", 2 * 2048 * 4096 * 11008),
+    ("fa_fwd2<ak::TF16, 128>", "flash_attention f16 causal [4,32,2048,128]", 2 * 2 * 4 * 32 * 128 * (2048 * 2049 // 2)),
 ]
 
 
@@ -88,10 +90,9 @@ def run_mfma() -> None:
     dev = torch.device("cuda:0")
     flush = torch.empty(512 * 2 ** 20, dtype=torch.uint8, device=dev)
     m = spec.baseline_matmul(device=dev)
-    Bt = m["B"].t().contiguous()
     f = spec.baseline_fused_mlp(device=dev)
     a = spec.baseline_attention(device=dev)
-    calls = [lambda: kernels.get("matmul")(m["A"], Bt.t()), lambda: kernels.get("fused_mlp")(**f),
+    calls = [lambda: kernels.get("matmul")(m["A"], m["B"]), lambda: kernels.get("fused_mlp")(**f),
              lambda: kernels.get("flash_attention")(**a)]
     for c in calls:
         for _ in range(3):

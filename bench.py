@@ -18,7 +18,8 @@ Also reported (same JSON line):
                 on a bounded sample of the same step, timed on this host.
   ops           every BASELINE workload (rmsnorm, rope, softmax, matmul, fused MLP, attention)
                 and the reference harness's primary sizes of layernorm / cross-entropy / reduce,
-                cold-cache timed (cache cleared before each call), vs stock PyTorch-ROCm.
+                cold-cache timed (cache cleared before each call), vs stock PyTorch-ROCm; first two
+                rows: a device copy of the bytes RoPE and softmax move (the practical ceiling).
   e2e           LLaMA-7B-shaped forward [1, 2048] f16, stock PyTorch vs all ops swapped.
 Progress goes to stderr.
 """
@@ -103,19 +104,29 @@ def op_table():
 
     def add(name, unit, work, fn, ref, note=""):
         t = harness.do_bench(fn)
-        tr = harness.do_bench(ref)
+        tr = harness.do_bench(ref) if ref is not None else None
         rate = work / (t["median"] * 1e-3) / (1e9 if unit == "GB/s" else 1e12)
         peak = HBM_PEAK_GBS if unit == "GB/s" else MFMA_PEAK_TFLOPS
         row = {"op": name, "median_us": round(t["median"] * 1e3, 2), "mean_us": round(t["mean"] * 1e3, 2),
-               "achieved": round(rate, 1), "unit": unit, "peak": peak, "frac": round(rate / peak, 4),
-               "torch_median_us": round(tr["median"] * 1e3, 2),
-               "speedup_vs_torch": round(tr["median"] / t["median"], 3)}
+               "achieved": round(rate, 1), "unit": unit, "peak": peak, "frac": round(rate / peak, 4)}
+        if tr is not None:
+            row["torch_median_us"] = round(tr["median"] * 1e3, 2)
+            row["speedup_vs_torch"] = round(tr["median"] / t["median"], 3)
         if note:
             row["note"] = note
         rows.append(row)
-        log(f"  {name:44s} {row['median_us']:9.1f} us  {rate:8.1f} {unit}  {100 * rate / peak:5.1f}%  "
-            f"torch {row['torch_median_us']:9.1f} us  x{row['speedup_vs_torch']}")
+        cmp = f"torch {row['torch_median_us']:9.1f} us  x{row['speedup_vs_torch']}" if tr is not None else ""
+        log(f"  {name:44s} {row['median_us']:9.1f} us  {rate:8.1f} {unit}  {100 * rate / peak:5.1f}%  {cmp}")
         torch.cuda.empty_cache()
+
+    # The practical HBM ceiling at the row ops' sizes, timed the same way: a device copy (torch) of
+    # the bytes RoPE (34 MB moved) and softmax (268 MB moved) move.
+    for n in (32 * 2048 * 128, 8192 * 8192):  # elements of the RoPE q tensor and the softmax input
+        src = torch.ones(n, device=dev, dtype=torch.float16)
+        dst = torch.empty_like(src)
+        add(f"device copy {2 * n * 2 / 1e6:.0f} MB moved (HBM reference)", "GB/s", 2 * n * 2,
+            lambda: dst.copy_(src), None, note="torch copy_, the practical ceiling at this size")
+        del src, dst
 
     i = spec.baseline_rmsnorm(device=dev)
     add("rmsnorm f16 [4096,4096] (C1)", "GB/s", (2 * 4096 * 4096 + 4096) * 2,

@@ -143,8 +143,8 @@ int ak_gemm(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t
 
 /*
  * 2-D transpose: dst[c][r] = src[r][c] for a rows x cols matrix with row strides ld_src / ld_dst.
- * No counterpart in the reference: the layout helper the matmul drop-in uses to feed a [K, N] B
- * operand to the K-contiguous GEMM path (one extra read and write of B).
+ * No counterpart in the reference: a layout helper for callers that keep a transposed copy of a
+ * matrix (ak_gemm itself reads both B layouts in place).
  */
 int ak_transpose(int dtype, const void* src, void* dst, int64_t rows, int64_t cols,
                  int64_t ld_src, int64_t ld_dst, hipStream_t stream);
