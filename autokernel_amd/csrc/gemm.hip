@@ -703,7 +703,9 @@ struct TileCfg {
 #endif
 static TileCfg pick_tile(int64_t M, int64_t N, int nb) {
   const TileCfg cands[] = {{256, 256}, {256, 128}, {128, 128}};
-  const double eff[] = {AK_GEMM_EFF256, 0.88, 0.80};
+  // relative per-flop throughput of the three tiles (bf16, MI355X): 4096^3 on 256x256 1230 TF/s,
+  // 2048x4096x4096 on 256x128 1084 TF/s, 2048x6144x4096 on 128x128 786 TF/s
+  const double eff[] = {AK_GEMM_EFF256, 0.88, 0.64};
   const int cus = 256;
   TileCfg best = cands[2];
   double best_s = -1.0;
@@ -803,10 +805,12 @@ static void launch_dma_cfg(const void* A, const void* B0, const void* B1, void* 
                            int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
   const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(N, BN);
   using P = DmaPlan<BM, BN, NB, WM * WN>;
-  // Four 32-deep stages when the grid leaves CUs idle (fewer tiles than CUs: each block's own DMA
-  // latency is then exposed; measured 2048x1024x4096: 50.9 us against 59.0 us two-stage).
+  // Four 32-deep stages when the grid fills at most half the CUs (each block's own DMA latency is
+  // then exposed; measured 2048x1024x4096: 50.9 us against 59.0 us two-stage). With more tiles the
+  // 64-deep pair is faster per tile (2048x6144x4096 on 192 tiles of 256x256: 109.9 us against
+  // 127.5 us).
   constexpr bool kOk32 = P::kOk32;
-  if (kOk32 && kUseDeep && tiles_m * tiles_n < kCUs) {
+  if (kOk32 && kUseDeep && 2 * tiles_m * tiles_n <= kCUs) {
     if constexpr (kOk32)
       launch_dma_kernel<T, BM, BN, WM, WN, NB, EPI, 32, 4, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, tiles_m,
                                                                 tiles_n, s);

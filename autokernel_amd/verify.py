@@ -145,6 +145,15 @@ class AttentionWrapper(nn.Module):
     def _proj(self, lin: nn.Linear, x):
         return _linear(x, lin.weight, lin.bias) if self.use_matmul else lin(x)
 
+    def _fp32_tables(self, cos: torch.Tensor, sin: torch.Tensor, T: int):
+        """Contiguous fp32 cos / sin [T, D/2], converted once per source table and length (the
+        model passes the same buffers to every layer and every call)."""
+        key = (cos.data_ptr(), cos._version, sin.data_ptr(), sin._version, cos.dtype, T)
+        cached = getattr(self, "_tab", None)
+        if cached is None or cached[0] != key:
+            self._tab = (key, cos[:T].float().contiguous(), sin[:T].float().contiguous())
+        return self._tab[1], self._tab[2]
+
     def forward(self, x, *rope_args):
         o = self.original
         B, T, _ = x.shape
@@ -160,8 +169,9 @@ class AttentionWrapper(nn.Module):
             v = self._proj(o.wv, x).view(B, T, Hk, D)
         cos, sin = _rope_tables_from(rope_args)
         if self.use_rope:
-            q = rope_mod.apply_fp32_tables(q, cos, sin)
-            k = rope_mod.apply_fp32_tables(k, cos, sin)
+            c32, s32 = self._fp32_tables(cos, sin, T)
+            q = rope_mod.apply_fp32_tables(q, c32, s32)
+            k = rope_mod.apply_fp32_tables(k, c32, s32)
         else:
             c, s = cos[:T].view(1, T, 1, -1), sin[:T].view(1, T, 1, -1)
 
