@@ -1,4 +1,4 @@
-// layout.hip -- 2-D transpose, the layout helper behind the [K, N] matmul operand.
+// layout.hip -- 2-D transpose (a layout helper) and a plain device copy (the bandwidth reference).
 //
 // dst[c][r] = src[r][c] for a rows x cols matrix. 64 x 64 tiles through LDS: 16-byte loads along
 // src rows, 16-byte stores along dst rows; the LDS tile has a padded pitch (66 halves) so the
@@ -72,9 +72,27 @@ __global__ __launch_bounds__(256) void transpose32(const float* __restrict__ src
   }
 }
 
+// One 16-byte vector per thread, all blocks in one pass. Measured on MI355X (cold cache) as the
+// fastest of 1, 4 and 8 vectors per thread, with or without nontemporal hints.
+__global__ __launch_bounds__(256) void copy16(const u32x4* __restrict__ src, u32x4* __restrict__ dst, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] = src[i];
+}
+
 }  // namespace ak
 
 using namespace ak;
+
+extern "C" int ak_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream) {
+  if (bytes < 0) return AK_EINVAL;
+  if (bytes == 0) return AK_OK;
+  if (!src || !dst) return AK_EINVAL;
+  if (bytes % 16 != 0 || !host_aligned16(src) || !host_aligned16(dst)) return AK_EUNSUPPORTED;
+  const int64_t n = bytes / 16, nb = cdiv(n, 256);
+  if (nb > INT_MAX) return AK_EINVAL;
+  copy16<<<(unsigned)nb, 256, 0, stream>>>((const u32x4*)src, (u32x4*)dst, n);
+  return record_launch();
+}
 
 extern "C" int ak_transpose(int dtype, const void* src, void* dst, int64_t rows, int64_t cols, int64_t ld_src,
                             int64_t ld_dst, hipStream_t stream) {

@@ -15,7 +15,8 @@ Also reported (same JSON line):
                 the timed region; traffic = HBM bytes per launch measured with rocprofv3 PMC
                 counters (profiles/traffic.json), or null when not measured.
   cpu_baseline  the CPU oracle (a restatement of the reference's reference.py on PyTorch CPU)
-                on a bounded sample of the same step, timed on this host.
+                on a bounded sample of the same step, timed on this host; each op row also
+                carries the same oracle's time for that op (cpu_ms, scaled from a stated sample).
   ops           every BASELINE workload (rmsnorm, rope, softmax, matmul, fused MLP, attention)
                 and the reference harness's primary sizes of layernorm / cross-entropy / reduce,
                 cold-cache timed (cache cleared before each call), vs stock PyTorch-ROCm; first two
@@ -119,13 +120,18 @@ def op_table():
         log(f"  {name:44s} {row['median_us']:9.1f} us  {rate:8.1f} {unit}  {100 * rate / peak:5.1f}%  {cmp}")
         torch.cuda.empty_cache()
 
-    # The practical HBM ceiling at the row ops' sizes, timed the same way: a device copy (torch) of
-    # the bytes RoPE (34 MB moved) and softmax (268 MB moved) move.
+    # The practical HBM ceiling at the row ops' sizes, timed the same way: a device copy (ak_copy,
+    # one 16-byte vector per thread) of the bytes RoPE (34 MB moved) and softmax (268 MB moved) move.
+    from autokernel_amd import _lib
     for n in (32 * 2048 * 128, 8192 * 8192):  # elements of the RoPE q tensor and the softmax input
         src = torch.ones(n, device=dev, dtype=torch.float16)
         dst = torch.empty_like(src)
-        add(f"device copy {2 * n * 2 / 1e6:.0f} MB moved (HBM reference)", "GB/s", 2 * n * 2,
-            lambda: dst.copy_(src), None, note="torch copy_, the practical ceiling at this size")
+
+        def copy(src=src, dst=dst):
+            _lib.check(_lib.load().ak_copy(src.data_ptr(), dst.data_ptr(), src.numel() * 2,
+                                           _lib.stream_of(src)), "ak_copy")
+        add(f"device copy {2 * n * 2 / 1e6:.0f} MB moved (HBM reference)", "GB/s", 2 * n * 2, copy,
+            lambda src=src, dst=dst: dst.copy_(src), note="ak_copy vs torch copy_: the practical ceiling at this size")
         del src, dst
 
     i = spec.baseline_rmsnorm(device=dev)
@@ -222,6 +228,60 @@ def cpu_baseline(seconds: float):
                                       f"{n} reps in {n * dt:.1f}s, oracle.reference_ops on PyTorch CPU"}
 
 
+def cpu_ops(min_seconds: float = 1.0):
+    """The reference's CPU path (oracle.reference_ops on PyTorch CPU, this host's cores) for each
+    op-table workload, on a stated fraction of it: one warm-up call, then the median of at least
+    three calls and at least `min_seconds` of calls, scaled to the full workload."""
+    import torch
+    from autokernel_amd import spec
+    from oracle import reference_ops as R
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    F16, BF16 = torch.float16, torch.bfloat16
+    out = {}
+
+    def timeit(key, frac, sample, fn):
+        fn()
+        ts, t_all = [], time.perf_counter()
+        while len(ts) < 3 or time.perf_counter() - t_all < min_seconds:
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+        ms = ts[len(ts) // 2] * 1e3 / frac
+        out[key] = {"cpu_ms": round(ms, 3), "cpu_sample": f"{sample}, {len(ts)} calls, median scaled x{1 / frac:g}"}
+        log(f"  cpu {key:44s} {ms:10.2f} ms ({sample})")
+
+    i = spec.baseline_rmsnorm(M=1024)
+    timeit("rmsnorm f16 [4096,4096] (C1)", 1024 / 4096, "1024 of 4096 rows",
+           lambda: R.rmsnorm_ref(i["x"], i["weight"], 1e-6))
+    r = spec.baseline_rope(H=4)
+    timeit("rotary_embedding f16 q [1,32,2048,128] (C2a)", 4 / 32, "4 of 32 heads",
+           lambda: R.rotary_embedding_ref(r["q"], r["cos"], r["sin"]))
+    x = spec.baseline_softmax(R=1024)["x"]
+    timeit("softmax f16 [8192,8192] (C2b)", 1024 / 8192, "1024 of 8192 rows", lambda: R.softmax_ref(x))
+    m = spec.baseline_matmul(M=512)
+    timeit("matmul bf16 4096^3 (C3a)", 512 / 4096, "512 of 4096 rows of A", lambda: R.matmul_ref(m["A"], m["B"]))
+    f = spec.baseline_fused_mlp(M=256)
+    timeit("fused_mlp bf16 x[2048,4096] H=11008 (C3b)", 256 / 2048, "256 of 2048 rows of x",
+           lambda: R.fused_mlp_ref(**f))
+    for B, S, hs in ((4, 2048, 4), (1, 8192, 1)):
+        a = spec.baseline_attention(B=1, H=hs, S=S)
+        timeit(f"flash_attention f16 causal [{B},32,{S},128] (C4)", hs / (32 * B), f"{hs} of {32 * B} (batch, head) pairs",
+               lambda: R.flash_attention_ref(a["Q"], a["K"], a["V"]))
+    g = torch.Generator().manual_seed(0)
+    xl = torch.randn(1024, 2048, generator=g).to(F16)
+    wl, bl = torch.ones(2048, dtype=F16), torch.zeros(2048, dtype=F16)
+    timeit("layernorm f16 [4096,2048] (harness large)", 1024 / 4096, "1024 of 4096 rows",
+           lambda: R.layernorm_ref(xl, wl, bl))
+    ce = spec.gen_cross_entropy({"batch": 512, "vocab": 32000}, F16, "cpu")
+    timeit("cross_entropy f16 [4096,32000] (harness large)", 512 / 4096, "512 of 4096 rows",
+           lambda: R.cross_entropy_ref(ce["logits"], ce["targets"]))
+    xr = spec.gen_reduce({"M": 1024, "N": 8192}, F16, "cpu")["x"]
+    timeit("reduce sum f16 [8192,8192] (harness large)", 1024 / 8192, "1024 of 8192 rows", lambda: R.reduce_sum_ref(xr))
+    del BF16
+    return out, torch.get_num_threads()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -271,6 +331,14 @@ def main() -> int:
     if args.cpu_seconds > 0:
         log("cpu baseline:")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        if "ops" in out:
+            cpu, threads = cpu_ops()
+            for row in out["ops"]:
+                c = cpu.get(row["op"])
+                if c:
+                    row.update(c)
+                    row["cpu_threads"] = threads
+                    row["speedup_vs_cpu"] = round(c["cpu_ms"] / (row["median_us"] / 1e3), 1)
     print(json.dumps(out), flush=True)
     return 0
 

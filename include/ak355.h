@@ -150,6 +150,13 @@ int ak_transpose(int dtype, const void* src, void* dst, int64_t rows, int64_t co
                  int64_t ld_src, int64_t ld_dst, hipStream_t stream);
 
 /*
+ * Device copy of `bytes` bytes (a multiple of 16, 16-byte aligned src and dst), one 16-byte vector
+ * per thread. No counterpart in the reference: the bandwidth reference the benchmark times beside
+ * the HBM-bound ops (the practical ceiling at a given size).
+ */
+int ak_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream);
+
+/*
  * Fused gate/up projection of the SwiGLU MLP:
  *   h = round(act(round(x @ w_gate.T))) * round(x @ w_up.T), rounded to the element type.
  * x: [M, D]; w_gate, w_up: [H, D] (nn.Linear layout); h: [M, H].

@@ -306,3 +306,14 @@ def test_transpose_layout_helper(gpu):
     big = torch.randn(128, 200, generator=g).half()
     view = big.to(gpu)[:, 8:136]  # row stride 200
     assert torch.equal(transpose(view).cpu(), big[:, 8:136].t().contiguous())
+
+
+def test_copy_reference_kernel(gpu):
+    """ak_copy (the bandwidth reference of the benchmark) copies bytes exactly, odd sizes included."""
+    from autokernel_amd import _lib
+    for n in (8, 4096 * 8 + 8, 1 << 22):
+        src = torch.randint(-30000, 30000, (n,), device=gpu, dtype=torch.int16)
+        dst = torch.zeros_like(src)
+        _lib.check(_lib.load().ak_copy(src.data_ptr(), dst.data_ptr(), n * 2, _lib.stream_of(src)), "ak_copy")
+        torch.cuda.synchronize()
+        assert torch.equal(src, dst)
