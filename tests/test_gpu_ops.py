@@ -253,7 +253,7 @@ def test_attention_rectangular_and_scale(gpu):
     K = torch.randn(1, 4, 160, 64, generator=g).bfloat16()
     V = torch.randn(1, 4, 160, 64, generator=g).bfloat16()
     for causal in (True, False):
-        for scale in (None, 0.05, 0.0):
+        for scale in (None, 0.05, 0.0, 1.0):  # 1.0: unscaled scores
             out = kernels.get("flash_attention")(Q.to(gpu), K.to(gpu), V.to(gpu), causal, scale)
             exp = R.flash_attention_ref(Q.float(), K.float(), V.float(), causal, scale)
             assert_close(out, exp, 2e-2, 2e-2, f"rect causal={causal} scale={scale}")
