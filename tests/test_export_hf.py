@@ -1,0 +1,171 @@
+"""HuggingFace Kernels ROCm export (autokernel_amd/export_hf.py; the reference's export_hf.py).
+
+CPU: the project layout, build.toml (ROCm backend, gfx950, HIP flags, every source listed and
+copied unchanged), the generated __init__.py, the kernel_fn signatures of _host.py against the
+in-tree kernel_fn modules, the CLI's error paths, and the torch binding that build() compiles
+from the exported project (every op registered with its schema; CPU tensors refused).
+GPU: every exported op through the compiled binding equals the in-tree kernel_fn bit for bit.
+"""
+from __future__ import annotations
+
+import ast
+import importlib.util
+import inspect
+
+import pytest
+import torch
+import tomli
+
+from autokernel_amd import build as B
+from autokernel_amd import export_hf as E
+from autokernel_amd import kernels, spec
+
+SCHEMAS = {
+    "rmsnorm": "(Tensor($0! -> ) y, Tensor x, Tensor weight, float eps) -> ()",
+    "layernorm": "(Tensor($0! -> ) y, Tensor x, Tensor? weight, Tensor? bias, float eps) -> ()",
+    "softmax": "(Tensor($0! -> ) y, Tensor x) -> ()",
+    "rope": "(Tensor($0! -> ) y, Tensor x, Tensor cos, Tensor sin, int rep_inner) -> ()",
+    "cross_entropy": "(Tensor($0! -> ) out, Tensor($1! -> ) row_loss, Tensor logits, Tensor targets, int ignore_index) -> ()",
+    "reduce_sum": "(Tensor($0! -> ) y, Tensor x, int outer, int reduce, int inner) -> ()",
+    "reduce_max": "(Tensor($0! -> ) y, Tensor x, int outer, int reduce, int inner) -> ()",
+    "gemm": "(Tensor($0! -> ) c, Tensor a, Tensor b, bool b_trans) -> ()",
+    "mlp_gate_up": "(Tensor($0! -> ) h, Tensor x, Tensor w_gate, Tensor w_up, int activation) -> ()",
+    "flash_attn_fwd": "(Tensor($0! -> ) o, Tensor q, Tensor k, Tensor v, bool causal, float sm_scale) -> ()",
+}
+
+
+def _load_host():
+    spec_ = importlib.util.spec_from_file_location("ak_hf_host", E.TEMPLATE_DIR / "host.py")
+    mod = importlib.util.module_from_spec(spec_)
+    spec_.loader.exec_module(mod)
+    return mod
+
+
+def test_export_all_layout_and_build_toml(tmp_path):
+    proj = E.export_kernel("ak_suite", tmp_path, repo_id="me/ak-suite", op="all", verbose=False)
+    cfg = tomli.loads((proj / "build.toml").read_text())
+    assert cfg["general"]["name"] == "ak_suite"
+    assert cfg["general"]["backends"] == ["rocm"]
+    assert cfg["general"]["hub"]["repo-id"] == "me/ak-suite"
+    assert cfg["torch"]["src"] == ["torch-ext/torch_binding.cpp", "torch-ext/torch_binding.h"]
+    k = cfg["kernel"]["ak_suite"]
+    assert k["backend"] == "rocm" and k["rocm-archs"] == ["gfx950"] and k["depends"] == ["torch"]
+    assert "-packed-fp32-ops" in k["hip-flags"] and "-O3" in k["hip-flags"]
+    assert not any(f.startswith("--offload-arch") for f in k["hip-flags"])
+    # every library source is listed, present and unchanged
+    want = {f"ak_suite_rocm/csrc/{p.name}" for p in B.CSRC.iterdir() if p.suffix in (".hip", ".h")}
+    assert set(k["src"]) == want | {"include/ak355.h"}
+    for rel in k["src"]:
+        orig = (E.HEADER if rel == "include/ak355.h" else B.CSRC / rel.rsplit("/", 1)[1])
+        assert (proj / rel).read_bytes() == orig.read_bytes(), rel
+    # ak_common.h reaches the header through ../../include from its own directory
+    assert (proj / "ak_suite_rocm" / "csrc" / "../../include/ak355.h").resolve().is_file()
+    for f in ("torch-ext/torch_binding.cpp", "torch-ext/torch_binding.h", "flake.nix", "README.md",
+              "torch-ext/ak_suite/_host.py"):
+        assert (proj / f).is_file(), f
+    assert "genKernelFlakeOutputs" in (proj / "flake.nix").read_text()
+    init = ast.parse((proj / "torch-ext/ak_suite/__init__.py").read_text())
+    names = {a.asname or a.name for n in ast.walk(init) if isinstance(n, ast.ImportFrom) for a in n.names}
+    assert set(E.OP_TYPES) <= names and "ops" in names
+
+
+def test_export_single_op_from_kernel_file(tmp_path):
+    kf = tmp_path / "kernel.py"
+    kf.write_text('KERNEL_TYPE = "softmax"\nfrom autokernel_amd.kernels.softmax import kernel_fn\n')
+    proj = E.export_kernel("ak_softmax", tmp_path / "out", kernel_path=kf, verbose=False)
+    init = (proj / "torch-ext/ak_softmax/__init__.py").read_text()
+    assert 'KERNEL_TYPE = "softmax"' in init and "kernel_fn = _host.KERNEL_FNS[KERNEL_TYPE]" in init
+    assert E.detect_kernel_type((E.REPO_ROOT / "kernel.py").read_text()) in E.OP_TYPES
+
+
+def test_export_errors(tmp_path, capsys):
+    with pytest.raises(ValueError):
+        E.export_kernel("not-an-identifier", tmp_path, op="rmsnorm", verbose=False)
+    with pytest.raises(ValueError):
+        E.export_kernel("ak_x", tmp_path, op="conv2d", verbose=False)
+    kf = tmp_path / "k.py"
+    kf.write_text("x = 1\n")
+    with pytest.raises(ValueError):
+        E.export_kernel("ak_x", tmp_path, kernel_path=kf, verbose=False)
+    assert E.main(["--name", "ak_x", "--op", "conv2d", "--output", str(tmp_path)]) == 1
+    assert "unknown op type" in capsys.readouterr().err
+    assert E.main(["--name", "ak_rms", "--op", "rmsnorm", "--output", str(tmp_path)]) == 0
+
+
+def test_host_signatures_match_kernel_fn():
+    host = _load_host()
+    assert set(host.KERNEL_FNS) == set(E.OP_TYPES) == set(spec.KERNEL_CONFIGS)
+    for op, fn in host.KERNEL_FNS.items():
+        mine = inspect.signature(fn).parameters
+        ref = inspect.signature(kernels.get(op)).parameters
+        assert [(p.name, p.default) for p in mine.values()] == [(p.name, p.default) for p in ref.values()], op
+    # every torch op a kernel_fn calls is registered by the binding
+    assert {o for v in E.OP_BINDINGS.values() for o in v} == set(SCHEMAS)
+
+
+def test_host_refuses_cpu_tensors():
+    host = _load_host()
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        host.rmsnorm(torch.randn(2, 8), torch.ones(8))
+
+
+def _ops_lib():
+    if not E.LOCAL_OPS_LIB.is_file():
+        pytest.fail(f"{E.LOCAL_OPS_LIB} is missing: run __graft_entry__.build() (or export_hf.build_local_ops())")
+    torch.ops.load_library(str(E.LOCAL_OPS_LIB))
+    return getattr(torch.ops, E.LOCAL_OPS_NAME)
+
+
+def test_binding_registers_every_op():
+    ns = _ops_lib()
+    for name, sig in SCHEMAS.items():
+        assert str(getattr(ns, name).default._schema) == f"{E.LOCAL_OPS_NAME}::{name}{sig}"
+    x = torch.randn(2, 8)
+    with pytest.raises(NotImplementedError):  # registered for the GPU dispatch key only
+        ns.rmsnorm(torch.empty_like(x), x, torch.ones(8), 1e-6)
+
+
+# ------------------------------------------------------------------------------------- GPU
+def _dev(v, gpu):
+    return v.to(gpu) if isinstance(v, torch.Tensor) else v
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("op", E.OP_TYPES)
+def test_exported_ops_match_kernels(gpu, op):
+    host = _load_host()
+    host.bind(_ops_lib())
+    cfg = spec.KERNEL_CONFIGS[op]
+    for dtype in cfg["test_dtypes"]:
+        inputs = {k: _dev(v, gpu) for k, v in cfg["input_generator"](spec.stage_size(cfg), dtype, "cpu", seed=7).items()}
+        want = kernels.get(op)(**inputs)
+        got = host.KERNEL_FNS[op](**inputs)
+        torch.cuda.synchronize()
+        assert got.shape == want.shape and got.dtype == want.dtype, (op, dtype)
+        assert torch.equal(got.cpu(), want.cpu()) or (
+            torch.equal(torch.isnan(got).cpu(), torch.isnan(want).cpu())
+            and torch.equal(got[~torch.isnan(got)].cpu(), want[~torch.isnan(want)].cpu())), (op, dtype)
+
+
+@pytest.mark.gpu
+def test_exported_layouts_match_kernels(gpu):
+    """The in-place layouts the binding passes strides for: [N, K] weights, strided A, GQA views,
+    dims other than the last."""
+    host = _load_host()
+    host.bind(_ops_lib())
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(300, 256, generator=g).half().to(gpu)
+    W = torch.randn(520, 256, generator=g).half().to(gpu)
+    assert torch.equal(host.matmul(x, W.t()), kernels.get("matmul")(x, W.t()))
+    big = torch.randn(300, 300, generator=g).half().to(gpu)
+    assert torch.equal(host.matmul(big[:, :256], W.t()), kernels.get("matmul")(big[:, :256], W.t()))
+    q = torch.randn(2, 200, 8, 128, generator=g).half().to(gpu).transpose(1, 2)
+    k = torch.randn(2, 200, 2, 128, generator=g).half().to(gpu).transpose(1, 2)
+    v = torch.randn(2, 200, 2, 128, generator=g).half().to(gpu).transpose(1, 2)
+    assert torch.equal(host.flash_attention(q, k, v, True), kernels.get("flash_attention")(q, k, v, True))
+    t = torch.randn(6, 70, 33, generator=g).half().to(gpu)
+    for d in (0, 1, -1):
+        assert torch.equal(host.reduce(t, d), kernels.get("reduce")(t, d))
+        assert torch.equal(host.reduce_max(t, d), kernels.reduce.reduce_max(t, d))
+        assert torch.equal(host.softmax(t, d), kernels.get("softmax")(t, d))
+    assert torch.equal(host.layernorm(t, None, None), kernels.get("layernorm")(t, None, None))
