@@ -410,33 +410,41 @@ __device__ __forceinline__ float fa2_halves_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// fa_fwd2 work split: kFa2Waves waves of 32 query rows per block, two waves per SIMD.
+#ifndef AK_FA2_WAVES
+#define AK_FA2_WAVES 4
+#endif
+constexpr int kFa2Waves = AK_FA2_WAVES;
+constexpr int kFa2BQ = 32 * kFa2Waves;
+constexpr int kFa2Threads = 64 * kFa2Waves;
+
 template <typename T, int D>
-__global__ __launch_bounds__(kFaThreads, 2) void fa_fwd2(
+__global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, int Hq, int group, int Sq, int Sk, int64_t qsb, int64_t qsh,
     int64_t qss, int64_t ksb, int64_t ksh, int kss, int64_t vsb, int64_t vsh, int vss,
     int64_t osb, int64_t osh, int64_t oss, int causal, float c_log2, float thr, int nbh) {
-  static_assert(kFaWaves == 4 && kFaBKV == 64, "fa_fwd2 tiling");
+  static_assert((kFa2Waves == 4 || kFa2Waves == 8) && kFaBKV == 64, "fa_fwd2 tiling");
   constexpr int DC = D / 8;             // 16-byte chunks per row
   constexpr int RPI = 64 / DC;          // rows per 1 KB DMA transfer
-  constexpr int NIW = kFaBKV / RPI / kFaWaves;  // transfers per wave per tile, per matrix
+  constexpr int NIW = kFaBKV / RPI / kFa2Waves;  // transfers per wave per tile, per matrix
   constexpr int NS = D / 16;            // 16-deep d steps of S^T
   constexpr int NDB = D / 32;           // 32-row d blocks of O^T
   constexpr int TILE = kFaBKV * D;      // elements of one K or V tile
-  static_assert(NIW * RPI * kFaWaves == kFaBKV, "tile rows split over waves");
+  static_assert(NIW * RPI * kFa2Waves == kFaBKV, "tile rows split over waves");
   __shared__ __attribute__((aligned(1024))) uint16_t sK[2 * TILE];
   __shared__ __attribute__((aligned(1024))) uint16_t sV[2 * TILE];
 
   const int bh = (int)(blockIdx.x % (unsigned)nbh);
   const int qi = (int)(blockIdx.x / (unsigned)nbh);
-  const int nqb = (Sq + kFaBQ - 1) / kFaBQ;
+  const int nqb = (Sq + kFa2BQ - 1) / kFa2BQ;
   const int qb = causal ? (nqb - 1 - qi) : qi;
   const int h = bh % Hq, b = bh / Hq;
   const int hk = h / group;
   const int lane = lane_id();
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
   const int l32 = lane & 31, hh = lane >> 5;
-  const int q0 = qb * kFaBQ;
+  const int q0 = qb * kFa2BQ;
   const int qw0 = q0 + w * 32;
   const int my_q = qw0 + l32;
 
@@ -451,7 +459,7 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fwd2(
   for (int s = 0; s < NS; ++s)
     qf[s] = (my_q < Sq) ? ld16(Qb + (int64_t)my_q * qss + s * 16 + hh * 8) : u32x4{0u, 0u, 0u, 0u};
 
-  const int kend = causal ? min(Sk, q0 + kFaBQ) : Sk;
+  const int kend = causal ? min(Sk, q0 + kFa2BQ) : Sk;
   const int nt = (kend + kFaBKV - 1) / kFaBKV;           // >= 1
   const int jw = causal ? min(nt - 1, (qw0 + 31) / kFaBKV) : nt - 1;  // this wave's last tile
 
@@ -461,7 +469,7 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fwd2(
   uint32_t offk[NIW], offv[NIW];
 #pragma unroll
   for (int i = 0; i < NIW; ++i) {
-    const int row = (i * kFaWaves + w) * RPI + lane / DC;
+    const int row = (i * kFa2Waves + w) * RPI + lane / DC;
     const int pc = lane % DC;
     offk[i] = (uint32_t)(row * kss * 2 + ((pc ^ fa2_kswz<D>(row)) * 16));
     offv[i] = (uint32_t)(row * vss * 2 + ((pc ^ fa2_vswz<D>(row)) * 16));
@@ -473,13 +481,13 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fwd2(
     const int k0 = j * kFaBKV;
     const u32x4 rs = fa2_rsrc(Kb + (int64_t)k0 * kss, (uint32_t)(((Sk - 1 - k0) * kss + D) * 2));
 #pragma unroll
-    for (int i = 0; i < NIW; ++i) fa2_dma16(rs, offk[i], sK_lds + stage * TILE * 2 + (i * kFaWaves + w) * 1024);
+    for (int i = 0; i < NIW; ++i) fa2_dma16(rs, offk[i], sK_lds + stage * TILE * 2 + (i * kFa2Waves + w) * 1024);
   };
   auto issue_v = [&](int j, int stage) {
     const int k0 = j * kFaBKV;
     const u32x4 rs = fa2_rsrc(Vb + (int64_t)k0 * vss, (uint32_t)(((Sk - 1 - k0) * vss + D) * 2));
 #pragma unroll
-    for (int i = 0; i < NIW; ++i) fa2_dma16(rs, offv[i], sV_lds + stage * TILE * 2 + (i * kFaWaves + w) * 1024);
+    for (int i = 0; i < NIW; ++i) fa2_dma16(rs, offv[i], sV_lds + stage * TILE * 2 + (i * kFa2Waves + w) * 1024);
   };
 
   // S^T = K Q^T for the 64 keys of a tile: two 32-key accumulators, issued alternately
@@ -745,6 +753,7 @@ static int launch_fa(const void* Q, const void* K, const void* V, void* O, int64
                      int64_t Hkv, int64_t Sq, int64_t Sk, const int64_t* qs, const int64_t* ks,
                      const int64_t* vs, const int64_t* os, int causal, float sm_scale, hipStream_t st) {
   const int64_t nblocks = cdiv(Sq, kFaBQ) * Hq * B;
+  const int64_t nblocks2 = cdiv(Sq, kFa2BQ) * Hq * B;
   if (nblocks > INT_MAX) return AK_EINVAL;
   const dim3 grid((unsigned)nblocks);
   // Scores whose f16 rounding (or f16 scaling by sm_scale) overflows become +-inf.
@@ -753,7 +762,7 @@ static int launch_fa(const void* Q, const void* K, const void* V, void* O, int64
   // byte offsets; anything else takes fa_fwd.
   const int64_t span = (int64_t)2 * Sk * (ks[2] > vs[2] ? ks[2] : vs[2]);
   if (sm_scale > 0.f && span < ((int64_t)1 << 31) && ks[2] >= D && vs[2] >= D) {
-    fa_fwd2<T, D><<<grid, kFaThreads, 0, st>>>(
+    fa_fwd2<T, D><<<dim3((unsigned)nblocks2), kFa2Threads, 0, st>>>(
         (const uint16_t*)Q, (const uint16_t*)K, (const uint16_t*)V, (uint16_t*)O, (int)Hq,
         (int)(Hq / Hkv), (int)Sq, (int)Sk, qs[0], qs[1], qs[2], ks[0], ks[1], (int)ks[2], vs[0],
         vs[1], (int)vs[2], os[0], os[1], os[2], causal, sm_scale * kFaLog2e,

@@ -183,6 +183,12 @@ def e2e(timed: int = 20, warm: int = 3):
     with verify.OptimizedModelContext(model, verify.ALL_KERNELS) as m:
         opt_out, opt_ms = verify.benchmark_model(m, ids, warm, timed)
     cmp = verify.compare_outputs(ref_out, opt_out, torch.float16, 1e-2, 1e-2)
+    # every op but attention: the reference verify's own check (f16 atol / rtol 1e-3, verify.py:51-54)
+    no_fa = tuple(k for k in verify.ALL_KERNELS if k != "flash_attention")
+    with torch.no_grad(), verify.OptimizedModelContext(model, no_fa) as m:
+        nofa_out = m(ids)
+    cmp_nofa = verify.compare_outputs(ref_out, nofa_out, torch.float16, 1e-3, 1e-3)
+    del nofa_out
     with torch.no_grad():
         m32 = llama.build("7b", torch.float32, dev)
         for p16, p32 in zip(model.parameters(), m32.parameters()):
@@ -196,7 +202,13 @@ def e2e(timed: int = 20, warm: int = 3):
            "speedup": round(ref_ms / opt_ms, 3),
            "vs_stock_allclose_1e-2": cmp["correctness"], "vs_stock_max_abs": cmp.get("max_abs_error"),
            "stock_vs_fp32_max_abs": round(e_stock.max().item(), 5), "stock_vs_fp32_mean_abs": round(e_stock.mean().item(), 6),
-           "ak_vs_fp32_max_abs": round(e_ak.max().item(), 5), "ak_vs_fp32_mean_abs": round(e_ak.mean().item(), 6)}
+           "ak_vs_fp32_max_abs": round(e_ak.max().item(), 5), "ak_vs_fp32_mean_abs": round(e_ak.mean().item(), 6),
+           "all_but_attention_vs_stock_allclose_1e-3": cmp_nofa["correctness"],
+           "all_but_attention_vs_stock_max_abs": cmp_nofa.get("max_abs_error"),
+           # attention is the one op that is not bit-identical to stock (SDPA); the accepted check is
+           # that the logits are at least as close to the fp32 model as stock f16's are (+10 %)
+           "vs_fp32_verdict": "PASS" if (e_ak.max() <= 1.1 * e_stock.max() and e_ak.mean() <= 1.1 * e_stock.mean())
+           else "FAIL"}
     del model
     torch.cuda.empty_cache()
     return res
