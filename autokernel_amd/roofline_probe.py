@@ -4,7 +4,7 @@ HBM traffic of the bandwidth-bound kernels (`run` / `summarize`) and MFMA / LDS 
 matrix kernels (`run_mfma` / `summarize_mfma`):
 
     rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE GRBM_GUI_ACTIVE \
-        -d DIR -o mfma_a --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma
+        --kernel-trace -d DIR -o mfma_a --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma
     rocprofv3 --pmc SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_WAIT_INST_LDS SQ_INSTS_MFMA SQ_INSTS_VALU SQ_INSTS_LDS SQ_WAVE_CYCLES \
         -d DIR -o mfma_b --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma
     python -m autokernel_amd.roofline_probe summarize_mfma DIR
@@ -74,12 +74,23 @@ def run() -> None:
     print("roofline_probe: done", flush=True)
 
 
-MFMA_PROBES = [  # kernel-name fragment, label, flops per launch
+SPEC_CLOCK_GHZ = 2.4  # MI355X peak engine clock, the clock the 2516.6 TFLOP/s dense figure assumes
+PEAK_TFLOPS = 2516.6
+# (kernel-name fragment, label, flops per launch, the call that launches it); each probe runs
+# three times in this order, so dispatches are assigned to probes by order and name
+MFMA_PROBES = [
     ("gemm_dma<ak::TBF16, 256, 256, 2, 4, 1, 0, 64, 2, true>", "matmul bf16 4096^3 (NN: [K, N] B, LDS-DMA)",
-     2 * 4096 ** 3),
-    ("gemm_dma<ak::TBF16, 256, 128, 2, 4, 2, 1", "fused_mlp gate/up bf16 2048x4096 H=11008", 2 * 2048 * 4096 * 11008 * 2),
-    ("gemm_dma<ak::TBF16, 256, 128, 4, 2, 1, 0", "fused_mlp down bf16 2048x4096 K=11008", 2 * 2048 * 4096 * 11008),
-    ("fa_fwd2<ak::TF16, 128>", "flash_attention f16 causal [4,32,2048,128]", 2 * 2 * 4 * 32 * 128 * (2048 * 2049 // 2)),
+     2 * 4096 ** 3, "matmul4k"),
+    ("gemm_dma<ak::TBF16, 256, 256, 2, 4, 1, 0, 64, 2, false>", "matmul bf16 8192^3 (NT: nn.Linear B, LDS-DMA)",
+     2 * 8192 ** 3, "matmul8k"),
+    ("gemm_dma<ak::TBF16, 256, 128, 2, 4, 2, 1", "fused_mlp gate/up bf16 2048x4096 H=11008",
+     2 * 2048 * 4096 * 11008 * 2, "mlp"),
+    ("gemm_dma<ak::TBF16, 256, 128, 4, 2, 1, 0", "fused_mlp down bf16 2048x4096 K=11008", 2 * 2048 * 4096 * 11008,
+     "mlp"),
+    ("fa_fwd2<ak::TF16, 128>", "flash_attention f16 causal [4,32,2048,128]", 2 * 2 * 4 * 32 * 128 * (2048 * 2049 // 2),
+     "fa2k"),
+    ("fa_fwd2<ak::TF16, 128>", "flash_attention f16 causal [1,32,8192,128]", 2 * 2 * 32 * 128 * (8192 * 8193 // 2),
+     "fa8k"),
 ]
 
 
@@ -90,46 +101,94 @@ def run_mfma() -> None:
     dev = torch.device("cuda:0")
     flush = torch.empty(512 * 2 ** 20, dtype=torch.uint8, device=dev)
     m = spec.baseline_matmul(device=dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    a8 = (torch.randn(8192, 8192, device=dev, generator=g) / 8192 ** 0.5).bfloat16()
+    w8 = torch.randn(8192, 8192, device=dev, generator=g).bfloat16()
     f = spec.baseline_fused_mlp(device=dev)
     a = spec.baseline_attention(device=dev)
-    calls = [lambda: kernels.get("matmul")(m["A"], m["B"]), lambda: kernels.get("fused_mlp")(**f),
-             lambda: kernels.get("flash_attention")(**a)]
-    for c in calls:
+    a_long = spec.baseline_attention(device=dev, B=1, S=8192)
+    calls = {"matmul4k": lambda: kernels.get("matmul")(m["A"], m["B"]),
+             "matmul8k": lambda: kernels.get("matmul")(a8, w8.t()),
+             "mlp": lambda: kernels.get("fused_mlp")(**f),
+             "fa2k": lambda: kernels.get("flash_attention")(**a),
+             "fa8k": lambda: kernels.get("flash_attention")(**a_long)}
+    for key in dict.fromkeys(p[3] for p in MFMA_PROBES):
         for _ in range(3):
             flush.zero_()
-            c()
+            calls[key]()
     torch.cuda.synchronize()
     print("roofline_probe: done", flush=True)
 
 
+def _dispatches(dirpath: str):
+    """[(dispatch id, kernel name, {counter: value}, duration ns or None)] in dispatch order, from
+    the counter_collection CSVs and, where the pass also ran --kernel-trace, its kernel_trace CSV."""
+    out = []
+    for path in glob.glob(os.path.join(dirpath, "**", "*counter_collection*.csv"), recursive=True):
+        dur = {}
+        kt = path.replace("counter_collection", "kernel_trace")
+        if os.path.exists(kt):
+            with open(kt) as f:
+                for row in csv.DictReader(f):
+                    dur[row["Dispatch_Id"]] = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+        per = {}
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                d = per.setdefault(row["Dispatch_Id"], (row["Kernel_Name"], defaultdict(float)))
+                d[1][row["Counter_Name"]] += float(row["Counter_Value"])
+        out.append([(int(i), n, dict(c), dur.get(i)) for i, (n, c) in per.items()])
+    return [sorted(o) for o in out]
+
+
 def summarize_mfma(dirpath: str) -> None:
-    data = _read(dirpath)
+    passes = _dispatches(dirpath)
+    # per probe: counters summed over the passes, durations from the pass that traced kernels
+    rows = []
+    for pi, (frag, label, flops, _) in enumerate(MFMA_PROBES):
+        ctr, durs = defaultdict(list), []
+        for disp in passes:
+            # probes with the same fragment take consecutive groups of three launches, in order
+            same = [x for x in disp if frag in x[1]]
+            k = sum(1 for q in MFMA_PROBES[:pi] if q[0] == frag)
+            for _, name, c, d in same[3 * k:3 * k + 3]:
+                for n, v in c.items():
+                    ctr[n].append(v)
+                if d:
+                    durs.append(d)
+        if not ctr:
+            continue
+        rows.append((frag, label, flops, {n: sum(v) / len(v) for n, v in ctr.items()},
+                     sum(durs) / len(durs) if durs else None))
+
     lines = ["# MFMA and LDS activity of the matrix kernels (rocprofv3 PMC)", "",
-             "Commands (two counter passes, then the summary):", "",
-             "    rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE GRBM_GUI_ACTIVE -d DIR -o mfma_a --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma",
+             "Commands (two counter passes, the first with the kernel trace, then the summary):", "",
+             "    rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE GRBM_GUI_ACTIVE --kernel-trace -d DIR -o mfma_a --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma",
              "    rocprofv3 --pmc SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_WAIT_INST_LDS SQ_INSTS_MFMA SQ_INSTS_VALU SQ_INSTS_LDS SQ_WAVE_CYCLES -d DIR -o mfma_b --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma",
              "    python -m autokernel_amd.roofline_probe summarize_mfma DIR", "",
-             "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 256 CUs x 4 SIMDs); LDS bank-conflict",
-             "rate = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE (the rocprof-compute definitions). Averages per dispatch.", "",
-             "| kernel | workload | MFMA busy | LDS bank-conflict rate | VALU active / wave-cycle | LDS active / wave-cycle | LDS wait / wave-cycle |",
-             "|---|---|---|---|---|---|---|"]
-
-    def avg(d, k):
-        v = d.get(k, [])
-        return sum(v) / len(v) if v else float("nan")
-
-    for frag, label, flops in MFMA_PROBES:
-        rows = [(k, v) for k, v in data.items() if frag in k]
-        if not rows:
-            continue
-        name, d = rows[0]
-        # GRBM_GUI_ACTIVE is summed over the 8 XCDs; MFMA busy cycles are counted per SIMD
-        busy = avg(d, "SQ_VALU_MFMA_BUSY_CYCLES") / (avg(d, "GRBM_GUI_ACTIVE") / 8 * 256 * 4)
-        conf = avg(d, "SQ_LDS_BANK_CONFLICT") / max(avg(d, "SQ_LDS_IDX_ACTIVE"), 1)
-        wc = max(avg(d, "SQ_WAVE_CYCLES"), 1)
-        lines.append(f"| {name.split('(')[0]} | {label} | {100 * busy:.1f}% | {100 * conf:.1f}% | "
-                     f"{avg(d, 'SQ_ACTIVE_INST_VALU') / wc:.3f} | {avg(d, 'SQ_ACTIVE_INST_LDS') / wc:.3f} | "
-                     f"{avg(d, 'SQ_WAIT_INST_LDS') / wc:.3f} |")
+             "* MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 256 CUs x 4 SIMDs).",
+             "* Sustained clock = GRBM_GUI_ACTIVE / 8 / kernel duration (same launch, profiled).",
+             f"* Clock-scaled peak = {PEAK_TFLOPS} TFLOP/s x clock / {SPEC_CLOCK_GHZ} GHz: what 100 % MFMA busy would give at",
+             "  the clock the kernel actually ran at. TFLOP/s here are from the profiled durations (counter",
+             "  collection slows kernels by a few percent; bench.py's figures are the unprofiled ones).",
+             "* LDS bank-conflict rate = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE (the rocprof-compute",
+             "  definition). Averages over three launches per workload, caches flushed before each.", "",
+             "| kernel | workload | TFLOP/s (profiled) | % of spec peak | sustained clock | MFMA busy | % of clock-scaled peak | LDS bank-conflict rate | VALU active / wave-cycle | LDS active / wave-cycle | LDS wait / wave-cycle |",
+             "|---|---|---|---|---|---|---|---|---|---|---|"]
+    for frag, label, flops, c, dur in rows:
+        grbm = c.get("GRBM_GUI_ACTIVE", float("nan")) / 8  # summed over the 8 XCDs
+        busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES", float("nan")) / (grbm * 256 * 4)
+        conf = c.get("SQ_LDS_BANK_CONFLICT", 0.0) / max(c.get("SQ_LDS_IDX_ACTIVE", 0.0), 1.0)
+        wc = max(c.get("SQ_WAVE_CYCLES", 0.0), 1.0)
+        if dur:
+            tf = flops / (dur * 1e-9) / 1e12
+            clk = grbm / (dur * 1e-9) / 1e9
+            perf = f"{tf:.0f} | {100 * tf / PEAK_TFLOPS:.1f}% | {clk:.2f} GHz"
+            scaled = f"{100 * tf / (PEAK_TFLOPS * clk / SPEC_CLOCK_GHZ):.1f}%"
+        else:
+            perf, scaled = "n/a | n/a | n/a", "n/a"
+        lines.append(f"| {frag.split('(')[0]} | {label} | {perf} | {100 * busy:.1f}% | {scaled} | {100 * conf:.1f}% | "
+                     f"{c.get('SQ_ACTIVE_INST_VALU', 0.0) / wc:.3f} | {c.get('SQ_ACTIVE_INST_LDS', 0.0) / wc:.3f} | "
+                     f"{c.get('SQ_WAIT_INST_LDS', 0.0) / wc:.3f} |")
     print("\n".join(lines))
 
 
