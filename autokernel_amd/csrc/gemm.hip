@@ -701,15 +701,21 @@ struct TileCfg {
 #ifndef AK_GEMM_EFF256
 #define AK_GEMM_EFF256 1.0
 #endif
-static TileCfg pick_tile(int64_t M, int64_t N, int nb) {
-  const TileCfg cands[] = {{256, 256}, {256, 128}, {128, 128}};
-  // relative per-flop throughput of the three tiles (bf16, MI355X): 4096^3 on 256x256 1230 TF/s,
-  // 2048x4096x4096 on 256x128 1084 TF/s, 2048x6144x4096 on 128x128 786 TF/s
-  const double eff[] = {AK_GEMM_EFF256, 0.88, 0.64};
+#ifndef AK_GEMM_EFF192
+#define AK_GEMM_EFF192 0.88
+#endif
+// wide192: also consider 256x192 tiles (the LDS-DMA kernel with nn.Linear-layout B; 2048 x 6144,
+// a fused QKV projection, is then exactly one tile per CU)
+static TileCfg pick_tile(int64_t M, int64_t N, int nb, bool wide192 = false) {
+  const TileCfg cands[] = {{256, 256}, {256, 128}, {128, 128}, {256, 192}};
+  // relative per-flop throughput of the tiles (bf16, MI355X): 4096^3 on 256x256 1230 TF/s,
+  // 2048x4096x4096 on 256x128 1084 TF/s, 2048x6144x4096 on 128x128 786 TF/s, on 256x192 1108 TF/s
+  const double eff[] = {AK_GEMM_EFF256, 0.88, 0.64, AK_GEMM_EFF192};
   const int cus = 256;
   TileCfg best = cands[2];
   double best_s = -1.0;
-  for (int i = 0; i < 3; ++i) {
+  const int ncand = (wide192 && nb == 1) ? 4 : 3;
+  for (int i = 0; i < ncand; ++i) {
     const int bn = cands[i].bn / (nb == 2 ? 2 : 1);
     const int64_t tiles = cdiv(M, cands[i].bm) * cdiv(N, bn);
     const int64_t waves = cdiv(tiles, cus);
@@ -823,8 +829,15 @@ static void launch_dma_cfg(const void* A, const void* B0, const void* B1, void* 
 template <typename T, int NB, int EPI, bool BKN>
 static void launch_gemm_dma(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
                             int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
-  const TileCfg t = pick_tile(M, N, NB);
+  // 256x192 needs [N, K] B: a [K, N] B tile row of 192 elements does not split into 1 KB transfers
+  const TileCfg t = pick_tile(M, N, NB, !BKN);
   if constexpr (NB == 1) {
+    if constexpr (!BKN) {
+      if (t.bm == 256 && t.bn == 192) {
+        launch_dma_cfg<T, 256, 192, 2, 4, 1, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+        return;
+      }
+    }
     if (t.bm == 256 && t.bn == 256)
       launch_dma_cfg<T, 256, 256, 2, kBigWN, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
     else if (t.bm == 256) launch_dma_cfg<T, 256, 128, 4, 2, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);

@@ -221,6 +221,18 @@ def test_matmul_linear_layout_and_strides(gpu):
     assert_close(kernels.get("matmul")(A.to(gpu), B.to(gpu)), R.matmul_ref(A.float(), B.float()).half(), 1e-2, 1e-2, "batched")
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 6144, 256), (500, 1100, 320), (256, 192, 64)])
+def test_matmul_linear_wide_tiles(gpu, M, N, K):
+    """nn.Linear-layout shapes whose best tiling is 256x192 (a fused QKV projection's 2048 x 6144,
+    ragged edges in M and N, a single tile) against the fp32 oracle."""
+    g = torch.Generator().manual_seed(M + N)
+    for dt in (torch.float16, torch.bfloat16):
+        x = (torch.randn(M, K, generator=g) / K ** 0.5).to(dt)
+        W = torch.randn(N, K, generator=g).to(dt)
+        out = kernels.get("matmul")(x.to(gpu), W.to(gpu).t())
+        assert_close(out, R.matmul_ref(x.float(), W.float().T).to(dt), 2e-2, 2e-2, f"{M}x{N}x{K} {dt}")
+
+
 def test_rope_model_layout(gpu):
     """[B, S, H, D] with cos [1, S, 1, D/2] (the layout a LLaMA block holds) reads the table per s."""
     g = torch.Generator().manual_seed(4)
