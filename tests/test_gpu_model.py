@@ -45,6 +45,45 @@ def test_small_llama_bit_exact_but_attention(gpu):
     assert verify.compare_outputs(ref, out, torch.float16, 1e-3, 1e-3)["correctness"] == "PASS"
 
 
+class _Gpt2Block(torch.nn.Module):
+    """A GPT-2-shaped block (pre-LayerNorm, fused c_attn, explicit softmax attention, GELU MLP):
+    the module-type swaps (nn.Linear -> matmul, nn.LayerNorm -> layernorm) of the reference
+    verify (verify.py:557-637) apply to it without a model-specific strategy."""
+
+    def __init__(self, dim, heads):
+        super().__init__()
+        self.heads = heads
+        self.ln_1, self.ln_2 = torch.nn.LayerNorm(dim), torch.nn.LayerNorm(dim)
+        self.c_attn, self.c_proj = torch.nn.Linear(dim, 3 * dim), torch.nn.Linear(dim, dim)
+        self.c_fc, self.mlp_proj = torch.nn.Linear(dim, 4 * dim), torch.nn.Linear(4 * dim, dim)
+
+    def forward(self, x):
+        B, T, C = x.shape
+        q, k, v = self.c_attn(self.ln_1(x)).split(C, dim=2)
+        q, k, v = (t.view(B, T, self.heads, C // self.heads).transpose(1, 2) for t in (q, k, v))
+        att = (q @ k.transpose(-2, -1).contiguous()) * (C // self.heads) ** -0.5
+        att = att.masked_fill(torch.ones(T, T, device=x.device, dtype=torch.bool).triu(1), float("-inf"))
+        y = (torch.softmax(att.float(), dim=-1).to(x.dtype) @ v).transpose(1, 2).reshape(B, T, C)
+        x = x + self.c_proj(y)
+        return x + self.mlp_proj(torch.nn.functional.gelu(self.c_fc(self.ln_2(x))))
+
+
+def test_gpt2_shaped_model_generic_swaps(gpu):
+    torch.manual_seed(0)
+    with torch.device(gpu):
+        m = torch.nn.Sequential(*[_Gpt2Block(256, 4) for _ in range(2)]).half().eval()
+        x = torch.randn(2, 96, 256).half()
+    with torch.no_grad():
+        ref = m(x)
+        ctx = verify.OptimizedModelContext(m, verify.ALL_KERNELS)
+        with ctx as pm:
+            out = pm(x)
+    assert ctx.applied == {"matmul": 8, "layernorm": 4}, ctx.applied
+    assert all(type(b.c_attn) is torch.nn.Linear for b in m), "modules restored on exit"
+    c = verify.compare_outputs(ref, out, torch.float16, 1e-2, 1e-2)
+    assert c["correctness"] == "PASS", c
+
+
 def test_model_form_norm_and_strided_rope(gpu):
     from autokernel_amd.kernels.rmsnorm import rms_norm_rsqrt
     from autokernel_amd.kernels.rotary_embedding import apply_fp32_tables
