@@ -417,6 +417,11 @@ __device__ __forceinline__ float fa2_halves_sum(float x) {
 constexpr int kFa2Waves = AK_FA2_WAVES;
 constexpr int kFa2BQ = 32 * kFa2Waves;
 constexpr int kFa2Threads = 64 * kFa2Waves;
+constexpr int kFa2Layer = 256;  // blocks per layer: one per MI355X compute unit
+#ifndef AK_FA_SNAKE
+#define AK_FA_SNAKE 1
+#endif
+constexpr bool kFaSnake = AK_FA_SNAKE != 0;
 
 template <typename T, int D>
 __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
@@ -435,8 +440,17 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   __shared__ __attribute__((aligned(1024))) uint16_t sK[2 * TILE];
   __shared__ __attribute__((aligned(1024))) uint16_t sV[2 * TILE];
 
-  const int bh = (int)(blockIdx.x % (unsigned)nbh);
-  const int qi = (int)(blockIdx.x / (unsigned)nbh);
+  // Causal work order: blocks come heaviest first (greedy balance over many rounds). A grid of at
+  // most two layers of kFa2Layer blocks (one block per CU each) reverses its second layer, so the
+  // two blocks that share a CU pair a heavy and a light query block (measured [1, 32, 2048, 128]:
+  // 56.2 -> 53.2 us; longer grids lose about 2 % with it). A bijection of block indices.
+  int L = (int)blockIdx.x;
+  if (kFaSnake && causal && gridDim.x <= 2u * kFa2Layer) {
+    const int layer = L / kFa2Layer, base = layer * kFa2Layer;
+    if (layer & 1) L = base + min(kFa2Layer, (int)gridDim.x - base) - 1 - (L - base);
+  }
+  const int bh = L % nbh;
+  const int qi = L / nbh;
   const int nqb = (Sq + kFa2BQ - 1) / kFa2BQ;
   const int qb = causal ? (nqb - 1 - qi) : qi;
   const int h = bh % Hq, b = bh / Hq;
