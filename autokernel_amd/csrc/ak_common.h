@@ -6,6 +6,7 @@
 // fp32 result into a half / bfloat16 tensor.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string.h>
@@ -183,6 +184,22 @@ __device__ __forceinline__ bool aligned16(const void* p) { return (((uintptr_t)p
 // Host-side helpers
 // ---------------------------------------------------------------------------------------------
 int record_launch(void);  // checks hipGetLastError(), stores its text, returns AK_OK / AK_EHIP
+
+// Start / stop events set by ak_set_launch_events for the calling thread's next timed launch
+// (null when none); taking them clears the slot.
+struct LaunchEvents {
+  hipEvent_t start, stop;
+};
+LaunchEvents take_launch_events(void);
+
+// Launch through hipExtLaunchKernelGGL when events are pending on this thread, so the dispatch
+// itself records them at the kernel's start and end; a plain launch otherwise.
+template <typename... Args, typename F = void (*)(Args...)>
+inline void launch_timed(F kernel, dim3 grid, dim3 block, uint32_t shmem, hipStream_t s, Args... args) {
+  const LaunchEvents e = take_launch_events();
+  if (e.start || e.stop) hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, e.start, e.stop, 0, args...);
+  else kernel<<<grid, block, shmem, s>>>(args...);
+}
 
 inline bool host_aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }

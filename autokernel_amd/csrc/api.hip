@@ -3,9 +3,17 @@
 
 namespace {
 thread_local char g_last_error[256] = "no error";
+// events the calling thread's next timed launch records (see ak_set_launch_events)
+thread_local hipEvent_t g_ev_start = nullptr, g_ev_stop = nullptr;
 }
 
 namespace ak {
+LaunchEvents take_launch_events(void) {
+  const LaunchEvents e{g_ev_start, g_ev_stop};
+  g_ev_start = g_ev_stop = nullptr;
+  return e;
+}
+
 int record_launch(void) {
   const hipError_t e = hipGetLastError();
   if (e == hipSuccess) return AK_OK;
@@ -28,3 +36,9 @@ extern "C" const char* ak_status_string(int status) {
 }
 
 extern "C" const char* ak_last_hip_error_string(void) { return g_last_error; }
+
+extern "C" int ak_set_launch_events(hipEvent_t start, hipEvent_t stop) {
+  g_ev_start = start;
+  g_ev_stop = stop;
+  return AK_OK;
+}

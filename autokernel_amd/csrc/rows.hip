@@ -312,10 +312,10 @@ static int launch_softmax(const void* x, void* y, int64_t rows, int64_t cols, hi
   if (vec && plan_row(cols / T::kVec, T::kVec, &plan)) {
     AK_ROW_SWITCH({
       const dim3 grid((unsigned)cdiv(rows, RowGeom<L>::kRowsPerBlock));
-      softmax_rows<T, L, VPT><<<grid, RowGeom<L>::kThreads, 0, s>>>(xp, yp, rows, (int)cols);
+      launch_timed(softmax_rows<T, L, VPT>, grid, dim3(RowGeom<L>::kThreads), 0, s, xp, yp, rows, (int)cols);
     });
   }
-  if (!handled) softmax_loop<T><<<(unsigned)rows, kLoopThreads, 0, s>>>(xp, yp, (int)cols);
+  if (!handled) launch_timed(softmax_loop<T>, dim3((unsigned)rows), dim3(kLoopThreads), 0, s, xp, yp, (int)cols);
   return record_launch();
 }
 

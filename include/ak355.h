@@ -51,6 +51,16 @@ const char* ak_status_string(int status);
 const char* ak_last_hip_error_string(void);
 
 /*
+ * Measurement hook: the calling thread's next timed launch (currently ak_softmax) records `start`
+ * and `stop` (created HIP events, or NULL) as part of its kernel dispatch, at the kernel's start
+ * and end, through hipExtLaunchKernel; the setting is then cleared. Event pairs recorded this way
+ * time the kernel alone, without the gap a separate hipEventRecord leaves before the dispatch.
+ * Per thread, so calls on other threads are unaffected. No counterpart in the reference: the
+ * benchmark's per-launch roofline timing.
+ */
+int ak_set_launch_events(hipEvent_t start, hipEvent_t stop);
+
+/*
  * RMSNorm over the last dim: y = (x / sqrt(mean(x*x) + eps)) * w, each step rounded to the
  * element type as the reference's tensor op sequence does.
  * x, y: [rows, cols]; w: [cols].

@@ -62,6 +62,7 @@ def test_invalid_arguments_rejected_on_host(lib):
     assert lib.ak_copy(x, x, 24, None) == _lib.AK_EUNSUPPORTED          # not a multiple of 16 bytes
     assert lib.ak_copy(ctypes.c_void_p(8), x, 16, None) == _lib.AK_EUNSUPPORTED  # misaligned
     assert lib.ak_copy(x, x, 0, None) == _lib.AK_OK
+    assert lib.ak_set_launch_events(None, None) == _lib.AK_OK  # clears this thread's slot
     assert lib.ak_rope(1, x, x, x, x, 4, 7, 4, 1, None) == _lib.AK_EINVAL   # odd head_dim
     assert lib.ak_gemm(1, x, x, x, 4, 4, 4, 2, 4, 4, 0, None) == _lib.AK_EINVAL  # lda < K
     assert lib.ak_mlp_gate_up(1, x, x, x, x, 4, 4, 4, 9, None) == _lib.AK_EINVAL  # activation code

@@ -271,6 +271,29 @@ def test_attention_rectangular_and_scale(gpu):
             assert_close(out, exp, 2e-2, 2e-2, f"rect causal={causal} scale={scale}")
 
 
+def test_softmax_dispatch_timed_events(gpu):
+    """ak_set_launch_events: the next softmax dispatch records the pair (a positive duration), the
+    result is the untimed launch's, and the setting applies to one launch only."""
+    from autokernel_amd import _lib
+    x = torch.randn(1024, 4096, generator=torch.Generator().manual_seed(9)).half().to(gpu)
+    want = kernels.get("softmax")(x)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    b.record()
+    torch.cuda.synchronize()
+    assert _lib.load().ak_set_launch_events(a.cuda_event, b.cuda_event) == _lib.AK_OK
+    got = kernels.get("softmax")(x)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b)
+    assert torch.equal(got, want)
+    assert 0.0 < ms < 50.0, ms
+    c = torch.cuda.Event(enable_timing=True)
+    c.record()
+    kernels.get("softmax")(x)  # untimed: leaves b as the first dispatch recorded it
+    torch.cuda.synchronize()
+    assert a.elapsed_time(b) == ms
+
+
 def test_reduce_other_dims_and_max(gpu):
     g = torch.Generator().manual_seed(7)
     x = torch.randn(6, 70, 33, generator=g).half()
