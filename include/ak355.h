@@ -5,7 +5,8 @@
  *   - takes device pointers, element counts and scalars only (no framework types);
  *   - launches asynchronously on the caller's HIP stream `stream` (pass torch's current stream);
  *   - never allocates, frees or synchronises; every buffer (outputs, workspaces) is the caller's;
- *   - keeps no mutable global state, so concurrent calls on different streams are safe;
+ *   - keeps no mutable global state, so concurrent calls on different streams are safe (the
+ *     one per-thread setting, ak_set_launch_events, affects only its own thread's next launch);
  *   - returns AK_OK or an ak_status code; AK_EHIP means a HIP launch error
  *     (its text is available from ak_last_hip_error_string() on the calling thread).
  *
