@@ -170,8 +170,14 @@ class AttentionWrapper(nn.Module):
         cos, sin = _rope_tables_from(rope_args)
         if self.use_rope:
             c32, s32 = self._fp32_tables(cos, sin, T)
-            q = rope_mod.apply_fp32_tables(q, c32, s32)
-            k = rope_mod.apply_fp32_tables(k, c32, s32)
+            if self.w_qkv is not None:
+                # q and k heads are adjacent in each token's row of the fused output: one launch
+                # rotates all H + Hk of them (the same per-element arithmetic as two calls)
+                qk = rope_mod.apply_fp32_tables(qkv[:, : (H + Hk) * D].view(B, T, H + Hk, D), c32, s32)
+                q, k = qk[:, :, :H], qk[:, :, H:]
+            else:
+                q = rope_mod.apply_fp32_tables(q, c32, s32)
+                k = rope_mod.apply_fp32_tables(k, c32, s32)
         else:
             c, s = cos[:T].view(1, T, 1, -1), sin[:T].view(1, T, 1, -1)
 
