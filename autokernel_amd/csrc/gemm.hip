@@ -95,7 +95,7 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int* tm, i
 // --------------------------------------------------------------------------------------------
 // Epilogues (applied to fp32 accumulators; every step rounds like the reference's tensor ops)
 // --------------------------------------------------------------------------------------------
-enum Epi { kEpiStore = 0, kEpiSilu = 1, kEpiGelu = 2, kEpiRelu2 = 3, kEpiNone = 4 };
+enum Epi { kEpiStore = 0, kEpiSilu = 1, kEpiGelu = 2, kEpiRelu2 = 3, kEpiNone = 4, kEpiResidual = 5 };
 
 template <typename T, int EPI>
 __device__ __forceinline__ float gate_up(float g_acc, float u_acc) {
@@ -107,6 +107,47 @@ __device__ __forceinline__ float gate_up(float g_acc, float u_acc) {
   else if constexpr (EPI == kEpiRelu2) { const float r = g > 0.f ? g : 0.f; a = T::rnd(r * r); }
   else a = g;
   return a * u;  // rounded by the store
+}
+
+// One lane's four consecutive outputs C[m][n .. n + 3] (element offset `off` of C[m][n]) from its
+// accumulators a0 (a1: the up accumulators when NB == 2). kEpiResidual rounds the product to the
+// element type, adds R[m][n + e] (R shares C's leading dimension) and rounds again: the two
+// roundings of torch's `R + A @ B`. fp32 holds the sum of two f16 / bf16 values to 24 bits, at
+// least 2p + 2 for both formats, so rounding it once more gives the correctly rounded sum.
+// VEC: C and R rows are 8-byte aligned, so four in-range columns move as one 8-byte access.
+template <typename T, int NB, int EPI, bool VEC>
+__device__ __forceinline__ void store_c4(uint16_t* __restrict__ C, const uint16_t* __restrict__ R, int64_t off,
+                                         int n, int N, const f32x4& a0, const f32x4& a1) {
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (NB == 2) v[e] = gate_up<T, EPI>(a0[e], a1[e]);
+    else if constexpr (EPI == kEpiResidual) v[e] = T::rnd(a0[e]);
+    else v[e] = a0[e];
+  }
+  const bool full = VEC && n + 3 < N;
+  if constexpr (NB == 1 && EPI == kEpiResidual) {
+    if (full) {
+      const u32x2 r = *reinterpret_cast<const u32x2*>(R + off);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += T::to_f((uint16_t)(r[e >> 1] >> ((e & 1) * 16)));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < N) v[e] += T::to_f(R[off + e]);
+    }
+  }
+  uint16_t* cp = C + off;
+  if (full) {
+    u32x2 o;
+    o[0] = (uint32_t)T::from_f(v[0]) | ((uint32_t)T::from_f(v[1]) << 16);
+    o[1] = (uint32_t)T::from_f(v[2]) | ((uint32_t)T::from_f(v[3]) << 16);
+    *reinterpret_cast<u32x2*>(cp) = o;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (n + e < N) cp[e] = T::from_f(v[e]);
+  }
 }
 
 // --------------------------------------------------------------------------------------------
@@ -273,23 +314,7 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma(
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int n = n0 + wn * WTN + j * 16 + fc * 4;
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if constexpr (NB == 1) v[e] = acc[0][i][j][e];
-        else v[e] = gate_up<T, EPI>(acc[0][i][j][e], acc[1][i][j][e]);
-      }
-      uint16_t* cp = C + (int64_t)m * ldc + n;
-      if (VEC && n + 3 < N) {
-        u32x2 o;
-        o[0] = (uint32_t)T::from_f(v[0]) | ((uint32_t)T::from_f(v[1]) << 16);
-        o[1] = (uint32_t)T::from_f(v[2]) | ((uint32_t)T::from_f(v[3]) << 16);
-        *reinterpret_cast<u32x2*>(cp) = o;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (n + e < N) cp[e] = T::from_f(v[e]);
-      }
+      store_c4<T, NB, EPI, VEC>(C, B1, (int64_t)m * ldc + n, n, N, acc[0][i][j], acc[NB - 1][i][j]);
     }
   }
 }
@@ -550,23 +575,7 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int n = n0 + wn * WTN + j * 16 + fc * 4;
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if constexpr (NB == 1) v[e] = acc[0][i][j][e];
-        else v[e] = gate_up<T, EPI>(acc[0][i][j][e], acc[1][i][j][e]);
-      }
-      uint16_t* cp = C + (int64_t)m * ldc + n;
-      if (n + 3 < N) {
-        u32x2 o;
-        o[0] = (uint32_t)T::from_f(v[0]) | ((uint32_t)T::from_f(v[1]) << 16);
-        o[1] = (uint32_t)T::from_f(v[2]) | ((uint32_t)T::from_f(v[3]) << 16);
-        *reinterpret_cast<u32x2*>(cp) = o;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (n + e < N) cp[e] = T::from_f(v[e]);
-      }
+      store_c4<T, NB, EPI, true>(C, B1, (int64_t)m * ldc + n, n, N, acc[0][i][j], acc[NB - 1][i][j]);
     }
   }
 }
@@ -1004,6 +1013,27 @@ extern "C" int ak_gemm(int dtype, const void* A, const void* B, void* C, int64_t
     case AK_F32: return launch_gemm32(A, B, C, M, N, K, lda, ldb, ldc, bt, stream);
     case AK_F16: return launch_gemm16<TF16, 1, kEpiStore>(A, B, nullptr, C, M, N, K, lda, ldb, ldc, bt, stream);
     case AK_BF16: return launch_gemm16<TBF16, 1, kEpiStore>(A, B, nullptr, C, M, N, K, lda, ldb, ldc, bt, stream);
+    default: return AK_EINVAL;
+  }
+}
+
+extern "C" int ak_gemm_residual(int dtype, const void* A, const void* B, const void* R, void* C, int64_t M,
+                                int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int b_trans,
+                                hipStream_t stream) {
+  if (M < 0 || N < 0 || K < 0 || M > INT_MAX || N > INT_MAX || K > INT_MAX) return AK_EINVAL;
+  if (M == 0 || N == 0) return AK_OK;
+  if (!A || !B || !R || !C) return AK_EINVAL;
+  if (lda < K || ldc < N || ldb < (b_trans ? K : N)) return AK_EINVAL;
+  if (cdiv(M, 128) * cdiv(N, 128) > INT_MAX) return AK_EINVAL;
+  // R is read and C written element by element in one pass: they must not overlap
+  const uintptr_t r0 = (uintptr_t)R, c0 = (uintptr_t)C;
+  const uintptr_t span = (uintptr_t)(((M - 1) * ldc + N) * 2);
+  if (r0 < c0 + span && c0 < r0 + span) return AK_EINVAL;
+  const bool bt = b_trans != 0;
+  switch (dtype) {
+    case AK_F16: return launch_gemm16<TF16, 1, kEpiResidual>(A, B, R, C, M, N, K, lda, ldb, ldc, bt, stream);
+    case AK_BF16: return launch_gemm16<TBF16, 1, kEpiResidual>(A, B, R, C, M, N, K, lda, ldb, ldc, bt, stream);
+    case AK_F32: return AK_EUNSUPPORTED;
     default: return AK_EINVAL;
   }
 }

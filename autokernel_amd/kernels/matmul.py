@@ -63,6 +63,30 @@ def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> t
     return C
 
 
+def gemm_residual(A: torch.Tensor, B: torch.Tensor, R: torch.Tensor) -> torch.Tensor:
+    """R + A @ B for 2-D A [M, K], B [K, N] (a transposed [N, K] view is read in place) and
+    R [M, N], f16 / bf16, in one ak_gemm_residual launch: the product is rounded, then the add,
+    so the result equals torch's `R + A @ B` bit for bit (models/llama_7b.py:110-111)."""
+    M, K = A.shape
+    K2, N = B.shape
+    if K != K2 or tuple(R.shape) != (M, N):
+        raise ValueError(f"gemm_residual: shapes {tuple(A.shape)} @ {tuple(B.shape)} + {tuple(R.shape)} do not align")
+    if not (A.dtype == B.dtype == R.dtype) or A.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"gemm_residual: needs one f16 / bf16 dtype, got {A.dtype}, {B.dtype}, {R.dtype}")
+    code = _lib.dtype_code(A, "gemm_residual")
+    if not (A.stride(1) == 1 and A.stride(0) >= max(K, 1)):
+        A = A.contiguous()
+    lda = A.stride(0) if M > 1 else max(K, 1)
+    Bt, ldb, bt = _b_layout(B)
+    R = R.contiguous()
+    C = torch.empty((M, N), device=A.device, dtype=A.dtype)
+    with device_guard(A):
+        st = _lib.load().ak_gemm_residual(code, A.data_ptr(), Bt.data_ptr(), R.data_ptr(), C.data_ptr(), M, N,
+                                          K, lda, ldb, max(N, 1), bt, _lib.stream_of(A))
+    _lib.check(st, "ak_gemm_residual", M=M, N=N, K=K, b_trans=bt, dtype=A.dtype)
+    return C
+
+
 def kernel_fn(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     _lib.require_gpu("matmul", A, B)
     if A.dim() == 1 and B.dim() == 1:

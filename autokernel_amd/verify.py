@@ -20,6 +20,9 @@ rotary embedding, attention and the SwiGLU MLP are added here):
                     ak_flash_attn_fwd on strided [B, T, H, D] views (no repeat_interleave, no
                     transpose copies)
   fused_mlp         SwiGLU feed-forward modules (w1 gate, w3 up, w2 down) -> ak_mlp_gate_up + ak_gemm
+  (with matmul)     pre-norm blocks (attention, feed_forward, attention_norm, ffn_norm) whose
+                    attention and feed-forward are swapped: each residual add runs in the epilogue
+                    of the GEMM that ends its branch (ak_gemm_residual), f16 / bf16
 """
 from __future__ import annotations
 
@@ -37,7 +40,8 @@ import torch.nn.functional as F
 from . import kernels
 from .kernels import flash_attention as fa_mod
 from .kernels import rotary_embedding as rope_mod
-from .kernels.matmul import gemm
+from .kernels.fused_mlp import gate_up
+from .kernels.matmul import gemm, gemm_residual
 from .kernels.rmsnorm import rms_norm_rsqrt
 
 ALL_KERNELS = ("matmul", "rmsnorm", "layernorm", "rotary_embedding", "flash_attention", "fused_mlp")
@@ -110,8 +114,19 @@ class FeedForwardWrapper(nn.Module):
         self.original = original
         self.gate, self.up, self.down = gate, up, down
 
-    def forward(self, x):
-        return kernels.get("fused_mlp")(x, self.gate.weight, self.up.weight, self.down.weight, "silu")
+    def forward(self, x, residual: Optional[torch.Tensor] = None):
+        if residual is None or not _fusable(residual):
+            y = kernels.get("fused_mlp")(x, self.gate.weight, self.up.weight, self.down.weight, "silu")
+            return y if residual is None else residual + y
+        x2 = x.reshape(-1, x.shape[-1]).contiguous()
+        h = gate_up(x2, self.gate.weight, self.up.weight, "silu")
+        y = gemm_residual(h, self.down.weight.t(), residual.reshape(-1, residual.shape[-1]))
+        return y.view(residual.shape)
+
+
+def _fusable(residual: torch.Tensor) -> bool:
+    """ak_gemm_residual serves f16 / bf16 (fp32 keeps the separate add)."""
+    return residual.dtype in (torch.float16, torch.bfloat16)
 
 
 def _rope_tables_from(args) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -154,7 +169,7 @@ class AttentionWrapper(nn.Module):
             self._tab = (key, cos[:T].float().contiguous(), sin[:T].float().contiguous())
         return self._tab[1], self._tab[2]
 
-    def forward(self, x, *rope_args):
+    def forward(self, x, *rope_args, residual: Optional[torch.Tensor] = None):
         o = self.original
         B, T, _ = x.shape
         H, Hk, D = self.n_heads, self.n_kv_heads, self.head_dim
@@ -197,7 +212,33 @@ class AttentionWrapper(nn.Module):
                 kh = kh.repeat_interleave(H // Hk, dim=1)
                 vh = vh.repeat_interleave(H // Hk, dim=1)
             y = F.scaled_dot_product_attention(qh, kh, vh, is_causal=True).transpose(1, 2).reshape(B, T, H * D)
-        return self._proj(o.wo, y)
+        if residual is None:
+            return self._proj(o.wo, y)
+        if self.use_matmul and o.wo.bias is None and _fusable(residual):
+            out = gemm_residual(y.reshape(B * T, H * D), o.wo.weight.t(), residual.reshape(B * T, -1))
+            return out.view(residual.shape)
+        return residual + self._proj(o.wo, y)
+
+
+class ResidualBlockWrapper(nn.Module):
+    """Pre-norm block x = x + attention(attention_norm(x)); x = x + feed_forward(ffn_norm(x))
+    (models/llama_7b.py:109-112) whose attention and feed-forward are libak355 wrappers: each
+    residual add is handed to the GEMM that ends its branch (the output projection, the down
+    projection), so it costs no launch of its own and gives the same bits as the separate add."""
+
+    def __init__(self, original: nn.Module):
+        super().__init__()
+        self.original = original
+
+    def forward(self, x, *args):
+        b = self.original
+        h = b.attention(b.attention_norm(x), *args, residual=x)
+        return b.feed_forward(b.ffn_norm(h), residual=h)
+
+
+def _is_prenorm_block(m: nn.Module) -> bool:
+    return all(isinstance(getattr(m, n, None), nn.Module)
+               for n in ("attention", "feed_forward", "attention_norm", "ffn_norm"))
 
 
 # ------------------------------------------------------------------------- module swapping
@@ -269,10 +310,19 @@ class OptimizedModelContext:
             elif "rmsnorm" in k and _is_rmsnorm(m):
                 self._set(name, RMSNormWrapper(m))
                 self._count("rmsnorm")
+        # blocks last: they call the (already swapped) submodules with their residuals
+        if "matmul" in k:
+            for name, m in modules:
+                if (name and _is_prenorm_block(m) and isinstance(m.attention, AttentionWrapper)
+                        and m.attention.use_matmul and isinstance(m.feed_forward, FeedForwardWrapper)):
+                    self._set(name, ResidualBlockWrapper(m))
+                    self._count("residual_block")
         return self.model
 
     def __exit__(self, *exc):
-        for name in sorted(self._orig, key=lambda n: -n.count(".")):
+        # newest swap first: a block wrapper goes before the submodules swapped inside its block,
+        # so each path below resolves through the original modules
+        for name in reversed(list(self._orig)):
             parent = self.model
             parts = name.split(".")
             for p in parts[:-1]:

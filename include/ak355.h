@@ -153,6 +153,18 @@ int ak_gemm(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t
             int64_t lda, int64_t ldb, int64_t ldc, int b_trans, hipStream_t stream);
 
 /*
+ * GEMM with the residual add of a transformer block in its epilogue: C = R + A * op(B), with
+ * A, B, b_trans, lda, ldb as in ak_gemm. The product is rounded to the element type, R is added
+ * and the sum rounded again, so C equals ak_gemm followed by a separate element-type add, bit for
+ * bit. R [M, N] has C's row stride ldc and must not overlap C. f16 / bf16 (fp32: AK_EUNSUPPORTED).
+ * Replaces: models/llama_7b.py:110-111 (x = x + attention(...), x = x + feed_forward(...)): the
+ *           output projections' GEMM plus the add kernel that follows it.
+ */
+int ak_gemm_residual(int dtype, const void* A, const void* B, const void* R, void* C, int64_t M,
+                     int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int b_trans,
+                     hipStream_t stream);
+
+/*
  * 2-D transpose: dst[c][r] = src[r][c] for a rows x cols matrix with row strides ld_src / ld_dst.
  * No counterpart in the reference: a layout helper for callers that keep a transposed copy of a
  * matrix (ak_gemm itself reads both B layouts in place).

@@ -65,6 +65,12 @@ def test_invalid_arguments_rejected_on_host(lib):
     assert lib.ak_set_launch_events(None, None) == _lib.AK_OK  # clears this thread's slot
     assert lib.ak_rope(1, x, x, x, x, 4, 7, 4, 1, None) == _lib.AK_EINVAL   # odd head_dim
     assert lib.ak_gemm(1, x, x, x, 4, 4, 4, 2, 4, 4, 0, None) == _lib.AK_EINVAL  # lda < K
+    y = ctypes.c_void_p(4096)
+    assert lib.ak_gemm_residual(1, x, x, x, x, 4, 4, 4, 4, 4, 4, 0, None) == _lib.AK_EINVAL  # R is C
+    assert lib.ak_gemm_residual(1, x, x, ctypes.c_void_p(40), x, 4, 4, 4, 4, 4, 4, 0, None) == _lib.AK_EINVAL
+    assert lib.ak_gemm_residual(1, x, x, None, y, 4, 4, 4, 4, 4, 4, 0, None) == _lib.AK_EINVAL
+    assert lib.ak_gemm_residual(0, x, x, x, y, 4, 4, 4, 4, 4, 4, 0, None) == _lib.AK_EUNSUPPORTED  # fp32
+    assert lib.ak_gemm_residual(1, x, x, x, y, 0, 4, 4, 4, 4, 4, 0, None) == _lib.AK_OK  # empty
     assert lib.ak_mlp_gate_up(1, x, x, x, x, 4, 4, 4, 9, None) == _lib.AK_EINVAL  # activation code
     assert lib.ak_reduce_max(1, x, x, 2, 0, 1, None) == _lib.AK_EINVAL      # max of nothing
     s = _lib.i64_array([8, 8, 8])

@@ -233,6 +233,29 @@ def test_matmul_linear_wide_tiles(gpu, M, N, K):
         assert_close(out, R.matmul_ref(x.float(), W.float().T).to(dt), 2e-2, 2e-2, f"{M}x{N}x{K} {dt}")
 
 
+@pytest.mark.parametrize("M,N,K,bt", [(300, 520, 256, True), (2048, 4096, 512, True), (130, 102, 96, True),
+                                      (257, 384, 128, False), (64, 200, 70, False)])
+def test_gemm_residual_equals_gemm_then_add(gpu, M, N, K, bt):
+    """ak_gemm_residual (LDS-DMA path, [K, N] B path, register-staged fallback for K % 64 != 0,
+    unaligned row strides) gives exactly ak_gemm followed by torch's element-type add, and the
+    oracle's R + A @ B within the matmul tolerance."""
+    from autokernel_amd.kernels.matmul import gemm, gemm_residual
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    for dt in (torch.float16, torch.bfloat16):
+        A = (torch.randn(M, K, generator=g) / K ** 0.5).to(dt)
+        W = torch.randn(N, K, generator=g).to(dt) if bt else torch.randn(K, N, generator=g).to(dt)
+        Rr = (torch.randn(M, N, generator=g) * 8).to(dt)
+        Rr[0, : min(N, 8)] = -0.0
+        Ad, Wd, Rd = A.to(gpu), W.to(gpu), Rr.to(gpu)
+        Bd = Wd.t() if bt else Wd
+        out = gemm_residual(Ad, Bd, Rd)
+        sep = Rd + gemm(Ad, Bd)
+        assert torch.equal(out, sep), f"{M}x{N}x{K} bt={bt} {dt}: fused add differs from the separate add"
+        B32 = W.float().T if bt else W.float()
+        exp = (Rr.float() + R.matmul_ref(A.float(), B32).to(dt).float()).to(dt)
+        assert_close(out, exp, 2e-2, 2e-2, f"{M}x{N}x{K} bt={bt} {dt}")
+
+
 def test_rope_model_layout(gpu):
     """[B, S, H, D] with cos [1, S, 1, D/2] (the layout a LLaMA block holds) reads the table per s."""
     g = torch.Generator().manual_seed(4)

@@ -15,12 +15,23 @@ def test_all_strategies_apply_and_restore():
     before = {n: type(x) for n, x in m.named_modules()}
     ctx = verify.OptimizedModelContext(m, verify.ALL_KERNELS)
     with ctx as pm:
-        assert ctx.applied == {"attention": 2, "fused_mlp": 2, "matmul": 1, "rmsnorm": 5}
-        assert isinstance(pm.layers[0].attention, verify.AttentionWrapper)
-        assert isinstance(pm.layers[1].feed_forward, verify.FeedForwardWrapper)
+        assert ctx.applied == {"attention": 2, "fused_mlp": 2, "matmul": 1, "rmsnorm": 5, "residual_block": 2}
+        assert isinstance(pm.layers[0], verify.ResidualBlockWrapper)
+        assert isinstance(pm.layers[0].original.attention, verify.AttentionWrapper)
+        assert isinstance(pm.layers[1].original.feed_forward, verify.FeedForwardWrapper)
         assert isinstance(pm.output, verify.LinearWrapper)
         assert isinstance(pm.norm, verify.RMSNormWrapper)
     assert {n: type(x) for n, x in m.named_modules()} == before
+
+
+def test_residual_blocks_need_swapped_branches():
+    """The residual fusion engages only where both branches are libak355 wrappers with GEMMs."""
+    for kinds, blocks in ((("matmul", "fused_mlp", "rotary_embedding"), 2), (("matmul", "fused_mlp"), 0),
+                          (("fused_mlp", "flash_attention"), 0), (("matmul", "flash_attention"), 0)):
+        m = tiny()
+        ctx = verify.OptimizedModelContext(m, kinds)
+        with ctx:
+            assert ctx.applied.get("residual_block", 0) == blocks, kinds
 
 
 def test_matmul_only_swaps_every_linear():
