@@ -41,6 +41,7 @@ SIGNATURES: dict[str, list] = {
     "ak_reduce_max": [_i, _p, _p, _i64, _i64, _i64, _p],
     "ak_gemm": [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],
     "ak_gemm_residual": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],
+    "ak_gemm_rope": [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p, _p, _i64, _i64, _i64, _p],
     "ak_mlp_gate_up": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i, _p],
     "ak_transpose": [_i, _p, _p, _i64, _i64, _i64, _i64, _p],
     "ak_copy": [_p, _p, _i64, _p],

@@ -95,7 +95,28 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int* tm, i
 // --------------------------------------------------------------------------------------------
 // Epilogues (applied to fp32 accumulators; every step rounds like the reference's tensor ops)
 // --------------------------------------------------------------------------------------------
-enum Epi { kEpiStore = 0, kEpiSilu = 1, kEpiGelu = 2, kEpiRelu2 = 3, kEpiNone = 4, kEpiResidual = 5 };
+enum Epi { kEpiStore = 0, kEpiSilu = 1, kEpiGelu = 2, kEpiRelu2 = 3, kEpiNone = 4, kEpiResidual = 5, kEpiRope = 6 };
+
+// Arguments of the rotary epilogue (kEpiRope), passed by value to every f16 / bf16 GEMM kernel:
+// columns [0, rot_cols) of C form heads of head_dim columns whose (even, odd) pairs are rotated
+// by the fp32 tables cos / sin [seq_len, head_dim / 2]; row m of C is token m % seq_len.
+struct EpiArgs {
+  const float* cos = nullptr;
+  const float* sin = nullptr;
+  int head_dim = 0;
+  int rot_cols = 0;
+  int seq_len = 1;
+};
+
+// The model's rotation of one pair in fp32, each product and sum rounded on its own (no fused
+// multiply-add), as separate fp32 tensor ops compute (a c - b s, a s + b c).
+__device__ __forceinline__ void rope_rotate(float& a, float& b, float c, float s) {
+#pragma clang fp contract(off)
+  const float y1 = a * c - b * s;
+  const float y2 = a * s + b * c;
+  a = y1;
+  b = y2;
+}
 
 template <typename T, int EPI>
 __device__ __forceinline__ float gate_up(float g_acc, float u_acc) {
@@ -109,44 +130,105 @@ __device__ __forceinline__ float gate_up(float g_acc, float u_acc) {
   return a * u;  // rounded by the store
 }
 
-// One lane's four consecutive outputs C[m][n .. n + 3] (element offset `off` of C[m][n]) from its
-// accumulators a0 (a1: the up accumulators when NB == 2). kEpiResidual rounds the product to the
-// element type, adds R[m][n + e] (R shares C's leading dimension) and rounds again: the two
-// roundings of torch's `R + A @ B`. fp32 holds the sum of two f16 / bf16 values to 24 bits, at
-// least 2p + 2 for both formats, so rounding it once more gives the correctly rounded sum.
+// Epilogue of one lane's share of a block tile: for fragment (i, j) the lane holds the four
+// consecutive outputs C[m][n .. n + 3], m = mb + 16 i, n = nb + 16 j, in acc[.][i][j] (NB == 2:
+// gate and up accumulators, combined by gate_up).
+//   kEpiResidual rounds the product to the element type, adds R[m][n + e] (R shares C's leading
+//     dimension) and rounds again: the two roundings of torch's `R + A @ B`. fp32 holds the sum of
+//     two f16 / bf16 values to 24 bits, at least 2p + 2 for both formats, so rounding it once more
+//     gives the correctly rounded sum.
+//   kEpiRope rounds the product to the element type, then (columns below rot_cols) rotates the
+//     pairs (n, n + 1), (n + 2, n + 3) in fp32 by table row m % seq_len and rounds once: the
+//     projection's output cast to fp32, rotated and cast back. n is a multiple of 4 and head_dim
+//     of 4, so the four columns never straddle a head or the rot_cols boundary.
+// The side values (R, or the cos / sin pairs) of every fragment are loaded first, then combined
+// and stored, so their latency is paid once per tile rather than once per fragment.
 // VEC: C and R rows are 8-byte aligned, so four in-range columns move as one 8-byte access.
-template <typename T, int NB, int EPI, bool VEC>
-__device__ __forceinline__ void store_c4(uint16_t* __restrict__ C, const uint16_t* __restrict__ R, int64_t off,
-                                         int n, int N, const f32x4& a0, const f32x4& a1) {
-  float v[4];
+template <typename T, int NB, int EPI, bool VEC, int FM, int FN>
+__device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const uint16_t* __restrict__ R,
+                                              int64_t ldc, int M, int N, int mb, int nb,
+                                              const f32x4 (&acc)[NB][FM][FN], const EpiArgs& ep) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  constexpr bool kRes = NB == 1 && EPI == kEpiResidual;
+  constexpr bool kRope = NB == 1 && EPI == kEpiRope;
+  u32x2 side_r[kRes ? FM : 1][kRes ? FN : 1];
+  f32x2 side_c[kRope ? FM : 1][kRope ? FN : 1], side_s[kRope ? FM : 1][kRope ? FN : 1];
+  if constexpr (kRes) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    if constexpr (NB == 2) v[e] = gate_up<T, EPI>(a0[e], a1[e]);
-    else if constexpr (EPI == kEpiResidual) v[e] = T::rnd(a0[e]);
-    else v[e] = a0[e];
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int m = mb + i * 16, n = nb + j * 16;
+        const uint16_t* rp = R + (int64_t)m * ldc + n;
+        u32x2 r = {0u, 0u};
+        if (m < M) {
+          if (VEC && n + 3 < N) {
+            r = *reinterpret_cast<const u32x2*>(rp);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < N) r[e >> 1] |= (uint32_t)rp[e] << ((e & 1) * 16);
+          }
+        }
+        side_r[i][j] = r;
+      }
   }
-  const bool full = VEC && n + 3 < N;
-  if constexpr (NB == 1 && EPI == kEpiResidual) {
-    if (full) {
-      const u32x2 r = *reinterpret_cast<const u32x2*>(R + off);
+  if constexpr (kRope) {
+    const int half = ep.head_dim >> 1;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] += T::to_f((uint16_t)(r[e >> 1] >> ((e & 1) * 16)));
-    } else {
+    for (int i = 0; i < FM; ++i) {
+      const int m = mb + i * 16;
+      const int64_t row = (int64_t)((m < M ? m : 0) % ep.seq_len) * half;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (n + e < N) v[e] += T::to_f(R[off + e]);
+      for (int j = 0; j < FN; ++j) {
+        const int n = nb + j * 16;
+        f32x2 c = {1.f, 1.f}, sn = {0.f, 0.f};
+        if (n < ep.rot_cols) {
+          const int64_t t = row + ((n % ep.head_dim) >> 1);  // even: 8-byte aligned pairs
+          c = *reinterpret_cast<const f32x2*>(ep.cos + t);
+          sn = *reinterpret_cast<const f32x2*>(ep.sin + t);
+        }
+        side_c[i][j] = c;
+        side_s[i][j] = sn;
+      }
     }
   }
-  uint16_t* cp = C + off;
-  if (full) {
-    u32x2 o;
-    o[0] = (uint32_t)T::from_f(v[0]) | ((uint32_t)T::from_f(v[1]) << 16);
-    o[1] = (uint32_t)T::from_f(v[2]) | ((uint32_t)T::from_f(v[3]) << 16);
-    *reinterpret_cast<u32x2*>(cp) = o;
-  } else {
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (n + e < N) cp[e] = T::from_f(v[e]);
+  for (int i = 0; i < FM; ++i) {
+    const int m = mb + i * 16;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = nb + j * 16;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (NB == 2) v[e] = gate_up<T, EPI>(acc[0][i][j][e], acc[1][i][j][e]);
+        else if constexpr (kRes || kRope) v[e] = T::rnd(acc[0][i][j][e]);
+        else v[e] = acc[0][i][j][e];
+      }
+      if constexpr (kRes) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += T::to_f((uint16_t)(side_r[i][j][e >> 1] >> ((e & 1) * 16)));
+      }
+      if constexpr (kRope) {
+        if (n < ep.rot_cols) {
+          rope_rotate(v[0], v[1], side_c[i][j][0], side_s[i][j][0]);
+          rope_rotate(v[2], v[3], side_c[i][j][1], side_s[i][j][1]);
+        }
+      }
+      uint16_t* cp = C + (int64_t)m * ldc + n;
+      if (VEC && n + 3 < N) {
+        u32x2 o;
+        o[0] = (uint32_t)T::from_f(v[0]) | ((uint32_t)T::from_f(v[1]) << 16);
+        o[1] = (uint32_t)T::from_f(v[2]) | ((uint32_t)T::from_f(v[3]) << 16);
+        *reinterpret_cast<u32x2*>(cp) = o;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) cp[e] = T::from_f(v[e]);
+      }
+    }
   }
 }
 
@@ -157,7 +239,7 @@ template <typename T, bool BT, bool VEC, int BM, int BN, int WM, int WN, int NB,
 __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B0, const uint16_t* __restrict__ B1,
     uint16_t* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
-    int tiles_m, int tiles_n) {
+    int tiles_m, int tiles_n, EpiArgs ep) {
   constexpr int kThreads = WM * WN * kWave;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
@@ -307,16 +389,7 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma(
   }
 
   // ---- epilogue: lane holds C[m][n .. n+3] for each (i, j) ----
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int m = m0 + wm * WTM + i * 16 + fr;
-    if (m >= M) continue;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int n = n0 + wn * WTN + j * 16 + fc * 4;
-      store_c4<T, NB, EPI, VEC>(C, B1, (int64_t)m * ldc + n, n, N, acc[0][i][j], acc[NB - 1][i][j]);
-    }
-  }
+  tile_epilogue<T, NB, EPI, VEC, FM, FN>(C, B1, ldc, M, N, m0 + wm * WTM + fr, n0 + wn * WTN + fc * 4, acc, ep);
 }
 
 // --------------------------------------------------------------------------------------------
@@ -503,7 +576,7 @@ template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, int BKD, 
 __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B0, const uint16_t* __restrict__ B1,
     uint16_t* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
-    int tiles_m, int tiles_n) {
+    int tiles_m, int tiles_n, EpiArgs ep) {
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
@@ -568,16 +641,7 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
                                                          sS0, sS1, sS2, sS3);
 
   const int fr = lane & 15, fc = lane >> 4;
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int m = m0 + wm * WTM + i * 16 + fr;
-    if (m >= M) continue;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int n = n0 + wn * WTN + j * 16 + fc * 4;
-      store_c4<T, NB, EPI, true>(C, B1, (int64_t)m * ldc + n, n, N, acc[0][i][j], acc[NB - 1][i][j]);
-    }
-  }
+  tile_epilogue<T, NB, EPI, true, FM, FN>(C, B1, ldc, M, N, m0 + wm * WTM + fr, n0 + wn * WTN + fc * 4, acc, ep);
 }
 
 // --------------------------------------------------------------------------------------------
@@ -742,11 +806,11 @@ static TileCfg pick_tile(int64_t M, int64_t N, int nb, bool wide192 = false) {
 
 template <typename T, bool BT, bool VEC, int BM, int BN, int WM, int WN, int NB, int EPI>
 static void launch_gemm_cfg(const void* A, const void* B0, const void* B1, void* C, int M, int N,
-                            int K, int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
+                            int K, int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s, const EpiArgs& ep) {
   const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(N, BN);
   gemm_mfma<T, BT, VEC, BM, BN, WM, WN, NB, EPI><<<tiles_m * tiles_n, WM * WN * kWave, 0, s>>>(
       (const uint16_t*)A, (const uint16_t*)B0, (const uint16_t*)B1, (uint16_t*)C, M, N, K, lda, ldb,
-      ldc, tiles_m, tiles_n);
+      ldc, tiles_m, tiles_n, ep);
 }
 
 // Waves along N of the 256x256 tile: 4 (8 waves of 128x64) or 2 (4 waves of 128x128, one wave
@@ -758,22 +822,22 @@ constexpr int kBigWN = AK_GEMM_BIG_WN;
 
 template <typename T, bool BT, bool VEC, int NB, int EPI>
 static void launch_gemm_tiled(const void* A, const void* B0, const void* B1, void* C, int M, int N,
-                              int K, int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
+                              int K, int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s, const EpiArgs& ep) {
   const TileCfg t = pick_tile(M, N, NB);
   if constexpr (NB == 1) {
     if (t.bm == 256 && t.bn == 256)
-      launch_gemm_cfg<T, BT, VEC, 256, 256, 2, kBigWN, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+      launch_gemm_cfg<T, BT, VEC, 256, 256, 2, kBigWN, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
     else if (t.bm == 256)
-      launch_gemm_cfg<T, BT, VEC, 256, 128, 4, 2, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+      launch_gemm_cfg<T, BT, VEC, 256, 128, 4, 2, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
     else
-      launch_gemm_cfg<T, BT, VEC, 128, 128, 2, 2, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+      launch_gemm_cfg<T, BT, VEC, 128, 128, 2, 2, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
   } else {
     if (t.bm == 256 && t.bn == 256)
-      launch_gemm_cfg<T, BT, VEC, 256, 128, 2, 4, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+      launch_gemm_cfg<T, BT, VEC, 256, 128, 2, 4, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
     else if (t.bm == 256)
-      launch_gemm_cfg<T, BT, VEC, 256, 64, 4, 2, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+      launch_gemm_cfg<T, BT, VEC, 256, 64, 4, 2, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
     else
-      launch_gemm_cfg<T, BT, VEC, 128, 64, 2, 2, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+      launch_gemm_cfg<T, BT, VEC, 128, 64, 2, 2, 2, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
   }
 }
 
@@ -789,10 +853,10 @@ constexpr int kCUs = 256;  // MI355X compute units
 
 template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, int BKD, int NS, bool BKN>
 static void launch_dma_kernel(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
-                              int64_t lda, int64_t ldb, int64_t ldc, int tiles_m, int tiles_n, hipStream_t s) {
+                              int64_t lda, int64_t ldb, int64_t ldc, int tiles_m, int tiles_n, hipStream_t s, const EpiArgs& ep) {
   gemm_dma<T, BM, BN, WM, WN, NB, EPI, BKD, NS, BKN><<<tiles_m * tiles_n, WM * WN * kWave, 0, s>>>(
       (const uint16_t*)A, (const uint16_t*)B0, (const uint16_t*)B1, (uint16_t*)C, M, N, K, lda, ldb, ldc,
-      tiles_m, tiles_n);
+      tiles_m, tiles_n, ep);
 }
 
 // Pipeline plan per tile shape: stage bytes (BM + NB * BN) * BKD * 2 and the 160 KB of LDS fix
@@ -817,7 +881,7 @@ struct DmaPlan {
 
 template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, bool BKN>
 static void launch_dma_cfg(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
-                           int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
+                           int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s, const EpiArgs& ep) {
   const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(N, BN);
   using P = DmaPlan<BM, BN, NB, WM * WN>;
   // Four 32-deep stages when the grid fills at most half the CUs (each block's own DMA latency is
@@ -828,42 +892,42 @@ static void launch_dma_cfg(const void* A, const void* B0, const void* B1, void* 
   if (kOk32 && kUseDeep && 2 * tiles_m * tiles_n <= kCUs) {
     if constexpr (kOk32)
       launch_dma_kernel<T, BM, BN, WM, WN, NB, EPI, 32, 4, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, tiles_m,
-                                                                tiles_n, s);
+                                                                tiles_n, s, ep);
     return;
   }
   launch_dma_kernel<T, BM, BN, WM, WN, NB, EPI, P::BKD, P::NS, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, tiles_m,
-                                                                    tiles_n, s);
+                                                                    tiles_n, s, ep);
 }
 
 template <typename T, int NB, int EPI, bool BKN>
 static void launch_gemm_dma(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
-                            int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
+                            int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s, const EpiArgs& ep) {
   // 256x192 needs [N, K] B: a [K, N] B tile row of 192 elements does not split into 1 KB transfers
   const TileCfg t = pick_tile(M, N, NB, !BKN);
   if constexpr (NB == 1) {
     if constexpr (!BKN) {
       if (t.bm == 256 && t.bn == 192) {
-        launch_dma_cfg<T, 256, 192, 2, 4, 1, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+        launch_dma_cfg<T, 256, 192, 2, 4, 1, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
         return;
       }
     }
     if (t.bm == 256 && t.bn == 256)
-      launch_dma_cfg<T, 256, 256, 2, kBigWN, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
-    else if (t.bm == 256) launch_dma_cfg<T, 256, 128, 4, 2, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
-    else launch_dma_cfg<T, 128, 128, 2, 2, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+      launch_dma_cfg<T, 256, 256, 2, kBigWN, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
+    else if (t.bm == 256) launch_dma_cfg<T, 256, 128, 4, 2, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
+    else launch_dma_cfg<T, 128, 128, 2, 2, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
   } else {
     static_assert(!BKN, "gate/up weights are [H, D]");
     if (t.bm == 256 && t.bn == 256)
-      launch_dma_cfg<T, 256, 128, 2, kBigWN, 2, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
-    else if (t.bm == 256) launch_dma_cfg<T, 256, 64, 4, 2, 2, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
-    else launch_dma_cfg<T, 128, 64, 2, 2, 2, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s);
+      launch_dma_cfg<T, 256, 128, 2, kBigWN, 2, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
+    else if (t.bm == 256) launch_dma_cfg<T, 256, 64, 4, 2, 2, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
+    else launch_dma_cfg<T, 128, 64, 2, 2, 2, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
   }
 }
 
 template <typename T, int NB, int EPI>
 static int launch_gemm16(const void* A, const void* B0, const void* B1, void* C, int64_t M,
                          int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, bool bt,
-                         hipStream_t s) {
+                         hipStream_t s, const EpiArgs& ep = EpiArgs{}) {
   bool vec = K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && host_aligned16(A) &&
              host_aligned16(B0) && (!B1 || host_aligned16(B1)) && (((uintptr_t)C) & 7u) == 0;
   if (!bt) vec = vec && N % 8 == 0;
@@ -871,24 +935,24 @@ static int launch_gemm16(const void* A, const void* B0, const void* B1, void* C,
   // LDS-DMA path: nn.Linear-layout B, K a multiple of 64, 32-bit element offsets
   const bool fits32 = M * lda < INT_MAX && N * ldb < INT_MAX;
   if (bt && vec && K % kBK == 0 && K > 0 && fits32 && kUseDma) {
-    launch_gemm_dma<T, NB, EPI, false>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s);
+    launch_gemm_dma<T, NB, EPI, false>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s, ep);
     return record_launch();
   }
   // [K, N] B (torch.matmul's layout) on the same pipeline, fragments read through LDS transposes
   if constexpr (NB == 1) {
     const bool fits32_kn = M * lda < INT_MAX && K * ldb < INT_MAX;
     if (!bt && vec && K % kBK == 0 && K > 0 && N >= 8 && fits32_kn && kUseDma) {
-      launch_gemm_dma<T, 1, EPI, true>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s);
+      launch_gemm_dma<T, 1, EPI, true>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s, ep);
       return record_launch();
     }
   }
   if (bt) {
-    if (vec) launch_gemm_tiled<T, true, true, NB, EPI>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s);
-    else launch_gemm_tiled<T, true, false, NB, EPI>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s);
+    if (vec) launch_gemm_tiled<T, true, true, NB, EPI>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s, ep);
+    else launch_gemm_tiled<T, true, false, NB, EPI>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s, ep);
   } else {
     if constexpr (NB == 1) {
-      if (vec) launch_gemm_tiled<T, false, true, 1, EPI>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s);
-      else launch_gemm_tiled<T, false, false, 1, EPI>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s);
+      if (vec) launch_gemm_tiled<T, false, true, 1, EPI>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s, ep);
+      else launch_gemm_tiled<T, false, false, 1, EPI>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s, ep);
     } else {
       return AK_EINVAL;
     }
@@ -1033,6 +1097,34 @@ extern "C" int ak_gemm_residual(int dtype, const void* A, const void* B, const v
   switch (dtype) {
     case AK_F16: return launch_gemm16<TF16, 1, kEpiResidual>(A, B, R, C, M, N, K, lda, ldb, ldc, bt, stream);
     case AK_BF16: return launch_gemm16<TBF16, 1, kEpiResidual>(A, B, R, C, M, N, K, lda, ldb, ldc, bt, stream);
+    case AK_F32: return AK_EUNSUPPORTED;
+    default: return AK_EINVAL;
+  }
+}
+
+extern "C" int ak_gemm_rope(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                            int64_t lda, int64_t ldb, int64_t ldc, int b_trans, const float* cos_t,
+                            const float* sin_t, int64_t seq_len, int64_t head_dim, int64_t rot_cols,
+                            hipStream_t stream) {
+  if (M < 0 || N < 0 || K < 0 || M > INT_MAX || N > INT_MAX || K > INT_MAX) return AK_EINVAL;
+  if (head_dim <= 0 || head_dim % 4 != 0 || head_dim > INT_MAX) return AK_EINVAL;
+  if (rot_cols < 0 || rot_cols > N || rot_cols % head_dim != 0) return AK_EINVAL;
+  if (seq_len <= 0 || seq_len > INT_MAX) return AK_EINVAL;
+  if (M == 0 || N == 0) return AK_OK;
+  if (!A || !B || !C || (rot_cols > 0 && (!cos_t || !sin_t))) return AK_EINVAL;
+  if ((((uintptr_t)cos_t) | ((uintptr_t)sin_t)) & 7u) return AK_EINVAL;  // pairs load as 8 bytes
+  if (lda < K || ldc < N || ldb < (b_trans ? K : N)) return AK_EINVAL;
+  if (cdiv(M, 128) * cdiv(N, 128) > INT_MAX) return AK_EINVAL;
+  EpiArgs ep;
+  ep.cos = cos_t;
+  ep.sin = sin_t;
+  ep.head_dim = (int)head_dim;
+  ep.rot_cols = (int)rot_cols;
+  ep.seq_len = (int)seq_len;
+  const bool bt = b_trans != 0;
+  switch (dtype) {
+    case AK_F16: return launch_gemm16<TF16, 1, kEpiRope>(A, B, nullptr, C, M, N, K, lda, ldb, ldc, bt, stream, ep);
+    case AK_BF16: return launch_gemm16<TBF16, 1, kEpiRope>(A, B, nullptr, C, M, N, K, lda, ldb, ldc, bt, stream, ep);
     case AK_F32: return AK_EUNSUPPORTED;
     default: return AK_EINVAL;
   }

@@ -87,6 +87,38 @@ def gemm_residual(A: torch.Tensor, B: torch.Tensor, R: torch.Tensor) -> torch.Te
     return C
 
 
+def gemm_rope(A: torch.Tensor, B: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, seq_len: int,
+              head_dim: int, rot_cols: int) -> torch.Tensor:
+    """A @ B (2-D, f16 / bf16) with the model's rotary embedding applied in the GEMM epilogue to
+    columns [0, rot_cols): each head of head_dim columns rotated pairwise in fp32 by the fp32
+    tables cos / sin [>= seq_len, head_dim / 2], row m being token m % seq_len, then rounded once.
+    One ak_gemm_rope launch; equals the projection followed by the fp32 rotation
+    (models/llama_7b.py:40-48, :67-71) bit for bit."""
+    M, K = A.shape
+    K2, N = B.shape
+    if K != K2:
+        raise ValueError(f"gemm_rope: shapes {tuple(A.shape)} and {tuple(B.shape)} do not align")
+    if A.dtype != B.dtype or A.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"gemm_rope: needs one f16 / bf16 dtype, got {A.dtype}, {B.dtype}")
+    half = head_dim // 2
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape[0] < seq_len or \
+            cos.shape[-1] != half or sin.shape != cos.shape:
+        raise ValueError(f"gemm_rope: tables must be fp32 [>= {seq_len}, {half}], got {tuple(cos.shape)} {cos.dtype}")
+    code = _lib.dtype_code(A, "gemm_rope")
+    if not (A.stride(1) == 1 and A.stride(0) >= max(K, 1)):
+        A = A.contiguous()
+    lda = A.stride(0) if M > 1 else max(K, 1)
+    Bt, ldb, bt = _b_layout(B)
+    c, s = cos.contiguous(), sin.contiguous()
+    C = torch.empty((M, N), device=A.device, dtype=A.dtype)
+    with device_guard(A):
+        st = _lib.load().ak_gemm_rope(code, A.data_ptr(), Bt.data_ptr(), C.data_ptr(), M, N, K, lda, ldb,
+                                      max(N, 1), bt, c.data_ptr(), s.data_ptr(), seq_len, head_dim, rot_cols,
+                                      _lib.stream_of(A))
+    _lib.check(st, "ak_gemm_rope", M=M, N=N, K=K, head_dim=head_dim, rot_cols=rot_cols, dtype=A.dtype)
+    return C
+
+
 def kernel_fn(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     _lib.require_gpu("matmul", A, B)
     if A.dim() == 1 and B.dim() == 1:

@@ -15,7 +15,8 @@ rotary embedding, attention and the SwiGLU MLP are added here):
   layernorm         nn.LayerNorm -> ak_layernorm
   rmsnorm           RMSNorm-like modules (by class name, or weight + eps, no bias, "...norm") ->
                     ak_rmsnorm_rsqrt for class RMSNorm (the model's rsqrt form), else ak_rmsnorm
-  rotary_embedding  inside attention: RoPE through ak_rope_f32_tables
+  rotary_embedding  inside attention: RoPE through ak_rope_f32_tables, or (with matmul, f16 / bf16)
+                    in the epilogue of the fused QKV GEMM (ak_gemm_rope)
   flash_attention   attention modules (wq / wk / wv / wo, n_heads, n_kv_heads) -> GQA-native
                     ak_flash_attn_fwd on strided [B, T, H, D] views (no repeat_interleave, no
                     transpose copies)
@@ -41,7 +42,7 @@ from . import kernels
 from .kernels import flash_attention as fa_mod
 from .kernels import rotary_embedding as rope_mod
 from .kernels.fused_mlp import gate_up
-from .kernels.matmul import gemm, gemm_residual
+from .kernels.matmul import gemm, gemm_residual, gemm_rope
 from .kernels.rmsnorm import rms_norm_rsqrt
 
 ALL_KERNELS = ("matmul", "rmsnorm", "layernorm", "rotary_embedding", "flash_attention", "fused_mlp")
@@ -173,8 +174,16 @@ class AttentionWrapper(nn.Module):
         o = self.original
         B, T, _ = x.shape
         H, Hk, D = self.n_heads, self.n_kv_heads, self.head_dim
+        cos, sin = _rope_tables_from(rope_args)
+        rotated = False
         if self.w_qkv is not None:
-            qkv = gemm(x.reshape(B * T, -1), self.w_qkv.t())
+            if self.use_rope and x.dtype in (torch.float16, torch.bfloat16) and D % 4 == 0:
+                # q and k heads rotated in the projection's epilogue: no RoPE launch of their own
+                c32, s32 = self._fp32_tables(cos, sin, T)
+                qkv = gemm_rope(x.reshape(B * T, -1), self.w_qkv.t(), c32, s32, T, D, (H + Hk) * D)
+                rotated = True
+            else:
+                qkv = gemm(x.reshape(B * T, -1), self.w_qkv.t())
             q = qkv[:, : H * D].view(B, T, H, D)
             k = qkv[:, H * D: (H + Hk) * D].view(B, T, Hk, D)
             v = qkv[:, (H + Hk) * D:].view(B, T, Hk, D)
@@ -182,8 +191,7 @@ class AttentionWrapper(nn.Module):
             q = self._proj(o.wq, x).view(B, T, H, D)
             k = self._proj(o.wk, x).view(B, T, Hk, D)
             v = self._proj(o.wv, x).view(B, T, Hk, D)
-        cos, sin = _rope_tables_from(rope_args)
-        if self.use_rope:
+        if self.use_rope and not rotated:
             c32, s32 = self._fp32_tables(cos, sin, T)
             if self.w_qkv is not None:
                 # q and k heads are adjacent in each token's row of the fused output: one launch
@@ -193,7 +201,7 @@ class AttentionWrapper(nn.Module):
             else:
                 q = rope_mod.apply_fp32_tables(q, c32, s32)
                 k = rope_mod.apply_fp32_tables(k, c32, s32)
-        else:
+        elif not self.use_rope:
             c, s = cos[:T].view(1, T, 1, -1), sin[:T].view(1, T, 1, -1)
 
             def rot(t):

@@ -165,6 +165,23 @@ int ak_gemm_residual(int dtype, const void* A, const void* B, const void* R, voi
                      hipStream_t stream);
 
 /*
+ * GEMM with the model's rotary embedding in its epilogue: C = A * op(B) (arguments as in ak_gemm),
+ * the product rounded to the element type; then, in columns [0, rot_cols), every head of head_dim
+ * columns has its (even, odd) pairs rotated in fp32 by cos / sin [seq_len, head_dim / 2] (fp32,
+ * contiguous; row m of C is token m % seq_len) and rounded once: y0 = x0 c - x1 s, y1 = x0 s + x1 c,
+ * each product and sum rounded in fp32. Columns from rot_cols on (v of a fused QKV projection)
+ * are plain products. Equals ak_gemm followed by ak_rope_f32_tables on those columns, bit for bit.
+ * head_dim a multiple of 4, rot_cols a multiple of head_dim and at most N; cos / sin 8-byte
+ * aligned. f16 / bf16.
+ * Replaces: models/llama_7b.py:67-71 (the wq / wk / wv projections and apply_rotary_emb,
+ *           models/llama_7b.py:40-48): the QKV GEMM plus the RoPE kernel that follows it.
+ */
+int ak_gemm_rope(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                 int64_t lda, int64_t ldb, int64_t ldc, int b_trans, const float* cos_t,
+                 const float* sin_t, int64_t seq_len, int64_t head_dim, int64_t rot_cols,
+                 hipStream_t stream);
+
+/*
  * 2-D transpose: dst[c][r] = src[r][c] for a rows x cols matrix with row strides ld_src / ld_dst.
  * No counterpart in the reference: a layout helper for callers that keep a transposed copy of a
  * matrix (ak_gemm itself reads both B layouts in place).

@@ -71,6 +71,14 @@ def test_invalid_arguments_rejected_on_host(lib):
     assert lib.ak_gemm_residual(1, x, x, None, y, 4, 4, 4, 4, 4, 4, 0, None) == _lib.AK_EINVAL
     assert lib.ak_gemm_residual(0, x, x, x, y, 4, 4, 4, 4, 4, 4, 0, None) == _lib.AK_EUNSUPPORTED  # fp32
     assert lib.ak_gemm_residual(1, x, x, x, y, 0, 4, 4, 4, 4, 4, 0, None) == _lib.AK_OK  # empty
+    rope = lib.ak_gemm_rope
+    assert rope(1, x, x, y, 4, 8, 4, 4, 4, 8, 1, x, x, 4, 6, 6, None) == _lib.AK_EINVAL  # head_dim % 4
+    assert rope(1, x, x, y, 4, 8, 4, 4, 4, 8, 1, x, x, 4, 4, 6, None) == _lib.AK_EINVAL  # rot_cols % head_dim
+    assert rope(1, x, x, y, 4, 8, 4, 4, 4, 8, 1, x, x, 4, 4, 12, None) == _lib.AK_EINVAL  # rot_cols > N
+    assert rope(1, x, x, y, 4, 8, 4, 4, 4, 8, 1, None, x, 4, 4, 8, None) == _lib.AK_EINVAL  # no table
+    assert rope(1, x, x, y, 4, 8, 4, 4, 4, 8, 1, x, x, 0, 4, 8, None) == _lib.AK_EINVAL  # seq_len
+    assert rope(0, x, x, y, 4, 8, 4, 4, 4, 8, 1, x, x, 4, 4, 8, None) == _lib.AK_EUNSUPPORTED  # fp32
+    assert rope(1, x, x, y, 0, 8, 4, 4, 4, 8, 1, x, x, 4, 4, 8, None) == _lib.AK_OK  # empty
     assert lib.ak_mlp_gate_up(1, x, x, x, x, 4, 4, 4, 9, None) == _lib.AK_EINVAL  # activation code
     assert lib.ak_reduce_max(1, x, x, 2, 0, 1, None) == _lib.AK_EINVAL      # max of nothing
     s = _lib.i64_array([8, 8, 8])

@@ -256,6 +256,32 @@ def test_gemm_residual_equals_gemm_then_add(gpu, M, N, K, bt):
         assert_close(out, exp, 2e-2, 2e-2, f"{M}x{N}x{K} bt={bt} {dt}")
 
 
+@pytest.mark.parametrize("Bt,T,heads,D,K,bt", [(2, 300, (8, 2, 2), 64, 512, True), (1, 130, (2, 1, 1), 128, 96, True),
+                                              (2, 128, (2, 2, 0), 64, 128, False)])
+def test_gemm_rope_equals_projection_then_rotation(gpu, Bt, T, heads, D, K, bt):
+    """ak_gemm_rope (LDS-DMA path, register-staged fallback for K % 64 != 0, [K, N] B) gives
+    exactly the projection followed by the model's fp32 rotation of the q / k columns, computed
+    with separate torch ops as the model does, and leaves the v columns as plain products."""
+    from autokernel_amd import llama
+    from autokernel_amd.kernels.matmul import gemm, gemm_rope
+    H, Hk, Hv = heads
+    N, rot = (H + Hk + Hv) * D, (H + Hk) * D
+    g = torch.Generator().manual_seed(T + D + K)
+    cos, sin = llama.rope_tables(D, T + 5)
+    for dt in (torch.float16, torch.bfloat16):
+        A = torch.randn(Bt * T, K, generator=g).to(dt)
+        W = (torch.randn(N, K, generator=g) * 0.05).to(dt)
+        Wd = W.to(gpu) if bt else W.t().contiguous().to(gpu)
+        Bm = Wd.t() if bt else Wd
+        c, s = cos.to(gpu), sin.to(gpu)
+        out = gemm_rope(A.to(gpu), Bm, c, s, T, D, rot)
+        plain = gemm(A.to(gpu), Bm)
+        qk = plain[:, :rot].view(Bt, T, H + Hk, D)
+        eq, _ = llama.apply_rotary_emb(qk, qk, c, s)
+        assert torch.equal(out[:, :rot], eq.reshape(Bt * T, rot)), f"rotated columns {dt}"
+        assert torch.equal(out[:, rot:], plain[:, rot:]), f"plain columns {dt}"
+
+
 def test_rope_model_layout(gpu):
     """[B, S, H, D] with cos [1, S, 1, D/2] (the layout a LLaMA block holds) reads the table per s."""
     g = torch.Generator().manual_seed(4)
