@@ -42,6 +42,24 @@ __device__ __forceinline__ f32x4 mfma16x16x32<TBF16>(const u32x4& a, const u32x4
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// The LDS-DMA kernel's MFMA in either shape: MF = 16 -> v_mfma_f32_16x16x32 (f32x4 accumulators),
+// MF = 32 -> v_mfma_f32_32x32x16 (f32x16). Both take 8 consecutive k of one row per lane.
+template <int MF>
+struct MfmaAcc { using type = f32x4; };
+template <>
+struct MfmaAcc<32> { using type = f32x16; };
+template <typename T, int MF>
+__device__ __forceinline__ typename MfmaAcc<MF>::type mfma_tile(const u32x4& a, const u32x4& b,
+                                                                const typename MfmaAcc<MF>::type& c) {
+  if constexpr (MF == 16) {
+    return mfma16x16x32<T>(a, b, c);
+  } else if constexpr (T::kCode == AK_F16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+}
+
 // Load 8 consecutive k of one row of a K-contiguous matrix (row stride ld). Out-of-range rows or
 // k give zeros. VEC: K, ld and the base are multiples of 8 elements / 16 bytes.
 template <bool VEC>
@@ -131,7 +149,7 @@ __device__ __forceinline__ float gate_up(float g_acc, float u_acc) {
 }
 
 // Epilogue of one lane's share of a block tile: for fragment (i, j) the lane holds the four
-// consecutive outputs C[m][n .. n + 3], m = mb + 16 i, n = nb + 16 j, in acc[.][i][j] (NB == 2:
+// consecutive outputs C[m][n .. n + 3], m = mb + MST i, n = nb + NST j, in acc[.][i][j] (NB == 2:
 // gate and up accumulators, combined by gate_up).
 //   kEpiResidual rounds the product to the element type, adds R[m][n + e] (R shares C's leading
 //     dimension) and rounds again: the two roundings of torch's `R + A @ B`. fp32 holds the sum of
@@ -144,7 +162,7 @@ __device__ __forceinline__ float gate_up(float g_acc, float u_acc) {
 // The side values (R, or the cos / sin pairs) of every fragment are loaded first, then combined
 // and stored, so their latency is paid once per tile rather than once per fragment.
 // VEC: C and R rows are 8-byte aligned, so four in-range columns move as one 8-byte access.
-template <typename T, int NB, int EPI, bool VEC, int FM, int FN>
+template <typename T, int NB, int EPI, bool VEC, int FM, int FN, int MST = 16, int NST = 16>
 __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const uint16_t* __restrict__ R,
                                               int64_t ldc, int M, int N, int mb, int nb,
                                               const f32x4 (&acc)[NB][FM][FN], const EpiArgs& ep) {
@@ -158,7 +176,7 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const int m = mb + i * 16, n = nb + j * 16;
+        const int m = mb + i * MST, n = nb + j * NST;
         const uint16_t* rp = R + (int64_t)m * ldc + n;
         u32x2 r = {0u, 0u};
         if (m < M) {
@@ -177,11 +195,11 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
     const int half = ep.head_dim >> 1;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      const int m = mb + i * 16;
+      const int m = mb + i * MST;
       const int64_t row = (int64_t)((m < M ? m : 0) % ep.seq_len) * half;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const int n = nb + j * 16;
+        const int n = nb + j * NST;
         f32x2 c = {1.f, 1.f}, sn = {0.f, 0.f};
         if (n < ep.rot_cols) {
           const int64_t t = row + ((n % ep.head_dim) >> 1);  // even: 8-byte aligned pairs
@@ -195,11 +213,11 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
   }
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
-    const int m = mb + i * 16;
+    const int m = mb + i * MST;
     if (m >= M) continue;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const int n = nb + j * 16;
+      const int n = nb + j * NST;
       float v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -460,24 +478,27 @@ struct DmaB {
   static constexpr int kRows = BKN ? BKD : BN;   // tile rows per stage
 };
 
-template <typename T, int BM, int BN, int WM, int WN, int NB, int BKD, int NS, bool BKN>
+template <typename T, int BM, int BN, int WM, int WN, int NB, int BKD, int NS, bool BKN, int MF>
 __device__ __forceinline__ void gemm_dma_ns_kloop(
-    f32x4 (&acc)[NB][BM / WM / 16][BN / WN / 16], const uint16_t* A, const uint16_t* B0,
+    typename MfmaAcc<MF>::type (&acc)[NB][BM / WM / MF][BN / WN / MF], const uint16_t* A, const uint16_t* B0,
     const uint16_t* B1, const uint32_t* oa, const uint32_t* ob, uint32_t kb_step_b, int K, int wid,
     int wm, int wn, int lane, uint16_t* s0, uint16_t* s1, uint16_t* s2, uint16_t* s3) {
   using G = DmaGeom<BKD>;
   using GB = DmaB<BN, BKD, BKN>;
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int FM = WTM / MF, FN = WTN / MF;
   constexpr int A_INS = BM / G::RPI / NW;
   constexpr int B_INS = GB::kRows / GB::RPI / NW;
   constexpr int INS = A_INS + NB * B_INS;
   constexpr int H = FM / 2;
-  constexpr int STEPS = BKD / 32;  // k-steps of 32 per tile
+  constexpr int KS = MF == 16 ? 32 : 16;  // k per MFMA
+  constexpr int STEPS = BKD / KS;         // k-steps per tile
   static_assert(NS >= 2 && NS <= 4, "stages");
+  static_assert(MF == 16 || !BKN, "[K, N] B fragments are built for the 16x16x32 shape");
   const uint16_t* Bm[2] = {B0, B1};
-  const int fr = lane & 15, fc = lane >> 4;
+  // fragment row (lane % MF) and 16-byte k chunk (lane / MF) of this lane
+  const int fr = lane & (MF - 1), fc = lane / MF;
   uint16_t* const st[4] = {s0, s1, s2, s3};
 
   auto issue = [&](int kt, uint16_t* sp) {
@@ -494,11 +515,11 @@ __device__ __forceinline__ void gemm_dma_ns_kloop(
   };
   u32x4 fa[FM], fb[NB][FN], fbn[NB][FN];
   auto frag = [&](const uint16_t* base, int row, int s) -> u32x4 {
-    return *reinterpret_cast<const u32x4*>(&base[row * BKD + G::swz(row, s * 4 + fc) * 8]);
+    return *reinterpret_cast<const u32x4*>(&base[row * BKD + G::swz(row, s * (KS / 8) + fc) * 8]);
   };
   auto load_a = [&](const uint16_t* sp, int s, int i0, int i1) {
 #pragma unroll
-    for (int i = i0; i < i1; ++i) fa[i] = frag(sp, wm * WTM + i * 16 + fr, s);
+    for (int i = i0; i < i1; ++i) fa[i] = frag(sp, wm * WTM + i * MF + fr, s);
   };
   auto load_b = [&](const uint16_t* sp, int s, u32x4 (*dst)[FN]) {
 #pragma unroll
@@ -515,7 +536,7 @@ __device__ __forceinline__ void gemm_dma_ns_kloop(
           const u32x2 hi = lds_tr16(p + 4 * BN);  // rows + 4 share the swizzle
           dst[b][j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         } else {
-          dst[b][j] = frag(sp + (BM + b * BN) * BKD, wn * WTN + j * 16 + fr, s);
+          dst[b][j] = frag(sp + (BM + b * BN) * BKD, wn * WTN + j * MF + fr, s);
         }
       }
   };
@@ -525,7 +546,7 @@ __device__ __forceinline__ void gemm_dma_ns_kloop(
 #pragma unroll
       for (int i = i0; i < i1; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[b][i][j] = mfma16x16x32<T>(fb[b][j], fa[i], acc[b][i][j]);
+        for (int j = 0; j < FN; ++j) acc[b][i][j] = mfma_tile<T, MF>(fb[b][j], fa[i], acc[b][i][j]);
   };
   const int KT = K / BKD;
   // One k-step: first half of the MFMAs; at a tile's last step (cross) wait until the next tile
@@ -572,14 +593,14 @@ __device__ __forceinline__ void gemm_dma_ns_kloop(
   wait_vmcnt<0>();  // no DMA may still target this block's LDS when its waves end
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, int BKD, int NS, bool BKN>
+template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, int BKD, int NS, bool BKN, int MF>
 __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B0, const uint16_t* __restrict__ B1,
     uint16_t* __restrict__ C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
     int tiles_m, int tiles_n, EpiArgs ep) {
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int FM = WTM / MF, FN = WTN / MF;  // MFMA fragments per wave along M and N
   constexpr int RPI = DmaGeom<BKD>::RPI;  // tile rows per DMA instruction (1 KB)
   using GB = DmaB<BN, BKD, BKN>;
   constexpr int A_INS = BM / RPI / NW;  // DMA instructions per wave per tile for A
@@ -629,19 +650,41 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
   }
   const uint32_t kb_step_b = 2u * (uint32_t)BKD * (uint32_t)ldb;  // B bytes per k-tile ([K, N] B)
 
-  f32x4 acc[NB][FM][FN];
+  using Acc = typename MfmaAcc<MF>::type;
+  Acc acc[NB][FM][FN];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) acc[b][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < (int)(sizeof(Acc) / 4); ++e) acc[b][i][j][e] = 0.f;
 
-  gemm_dma_ns_kloop<T, BM, BN, WM, WN, NB, BKD, NS, BKN>(acc, A, B0, B1, oa, ob, kb_step_b, K, wid, wm, wn, lane,
-                                                         sS0, sS1, sS2, sS3);
+  gemm_dma_ns_kloop<T, BM, BN, WM, WN, NB, BKD, NS, BKN, MF>(acc, A, B0, B1, oa, ob, kb_step_b, K, wid, wm, wn,
+                                                             lane, sS0, sS1, sS2, sS3);
 
-  const int fr = lane & 15, fc = lane >> 4;
-  tile_epilogue<T, NB, EPI, true, FM, FN>(C, B1, ldc, M, N, m0 + wm * WTM + fr, n0 + wn * WTN + fc * 4, acc, ep);
+  if constexpr (MF == 16) {
+    // 16x16 fragment: lane holds C[m0' + lane % 16][n0' + 4 (lane / 16) + 0..3]
+    const int fr = lane & 15, fc = lane >> 4;
+    tile_epilogue<T, NB, EPI, true, FM, FN>(C, B1, ldc, M, N, m0 + wm * WTM + fr, n0 + wn * WTN + fc * 4, acc, ep);
+  } else {
+    // 32x32 fragment: lane holds C[m0' + lane % 32][n0' + 8 g + 4 (lane / 32) + 0..3], g = 0..3,
+    // in accumulator elements 4 g .. 4 g + 3: four 4-column groups 8 columns apart
+    f32x4 acc4[NB][FM][FN * 4];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            acc4[b][i][4 * j + g] = f32x4{acc[b][i][j][4 * g], acc[b][i][j][4 * g + 1], acc[b][i][j][4 * g + 2],
+                                          acc[b][i][j][4 * g + 3]};
+    tile_epilogue<T, NB, EPI, true, FM, FN * 4, 32, 8>(C, B1, ldc, M, N, m0 + wm * WTM + (lane & 31),
+                                                       n0 + wn * WTN + 4 * (lane >> 5), acc4, ep);
+  }
 }
 
 // --------------------------------------------------------------------------------------------
@@ -851,10 +894,20 @@ constexpr bool kUseDma = AK_GEMM_DMA != 0;
 constexpr bool kUseDeep = AK_GEMM_DEEP != 0;
 constexpr int kCUs = 256;  // MI355X compute units
 
+#ifndef AK_GEMM_MF
+#define AK_GEMM_MF 16
+#endif
+constexpr int kGemmMF = AK_GEMM_MF;
+
 template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, int BKD, int NS, bool BKN>
 static void launch_dma_kernel(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
-                              int64_t lda, int64_t ldb, int64_t ldc, int tiles_m, int tiles_n, hipStream_t s, const EpiArgs& ep) {
-  gemm_dma<T, BM, BN, WM, WN, NB, EPI, BKD, NS, BKN><<<tiles_m * tiles_n, WM * WN * kWave, 0, s>>>(
+                              int64_t lda, int64_t ldb, int64_t ldc, int tiles_m, int tiles_n, hipStream_t s,
+                              const EpiArgs& ep) {
+  // MFMA shape: 32x32x16 where the wave tile holds whole 32x32 fragments (an even count along M)
+  // and B is nn.Linear-layout; else 16x16x32
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int MF = (kGemmMF == 32 && !BKN && WTN % 32 == 0 && (WTM / 32) % 2 == 0) ? 32 : 16;
+  gemm_dma<T, BM, BN, WM, WN, NB, EPI, BKD, NS, BKN, MF><<<tiles_m * tiles_n, WM * WN * kWave, 0, s>>>(
       (const uint16_t*)A, (const uint16_t*)B0, (const uint16_t*)B1, (uint16_t*)C, M, N, K, lda, ldb, ldc,
       tiles_m, tiles_n, ep);
 }
