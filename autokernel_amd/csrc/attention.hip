@@ -762,6 +762,185 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   }
 }
 
+// ============================================================================================
+// fa_general: every case the two MFMA kernels do not serve -- fp32, and head_dim other than 64 or
+// 128 (any D up to 256) -- with the reference's arithmetic step by step (reference.py:32-42):
+//   s = rnd(rnd(q . k) * sm_scale)     the score matrix and its scaled value in the element type
+//   masked keys (causal, j > i) = -inf; P = rnd(softmax(s)) with fp32 statistics
+//   O = rnd(P V)                       fp32 accumulation, one rounding
+// rnd is the identity for fp32. Scores, products and sums are fp32 VALU work (f16 / bf16 products
+// are exact in fp32). Two passes over the keys: the first takes each query row's max and sum, the
+// second forms the normalised P, rounds it as F.softmax's output is rounded, and accumulates P V.
+// A row whose max is +-inf or NaN comes out NaN, as softmax makes it.
+// Work split: a block is 4 waves and 32 queries (8 per wave) of one (batch, head). Key tiles of
+// KT = 64 keys (32 for head_dim above 128, so the tiles fit LDS) are staged in LDS as fp32; for the
+// scores lane L takes key L % KT of query L / KT (+ 64 / KT per step), for P V lane L owns dims
+// L, L + 64, ... K rows are padded by one float, so the 64 lanes reading one dim of 64 rows hit 64
+// banks.
+// ============================================================================================
+constexpr int kFgWaves = 4, kFgQW = 8, kFgQB = kFgWaves * kFgQW;
+
+template <typename T, int DMAX>
+__global__ __launch_bounds__(kFgWaves * 64) void fa_general(
+    const typename T::S* __restrict__ Q, const typename T::S* __restrict__ K,
+    const typename T::S* __restrict__ V, typename T::S* __restrict__ O, int Hq, int group, int Sq, int Sk,
+    int D, int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb,
+    int64_t vsh, int64_t vss, int64_t osb, int64_t osh, int64_t oss, int causal, float scale, int nbh) {
+  constexpr int KT = DMAX > 128 ? 32 : 64;  // LDS holds fp32: 256-wide rows take 32-key tiles
+  constexpr int QPP = 64 / KT;        // queries scored side by side in one wave
+  constexpr int KP = DMAX + 1;        // padded K row in LDS (floats)
+  constexpr int RD = DMAX / 64;       // dims per lane in P V
+  static_assert(DMAX % 64 == 0 && kFgQW % QPP == 0, "fa_general tiling");
+  __shared__ float sQ[kFgQB * DMAX];
+  __shared__ float sK[KT * KP];
+  __shared__ float sV[KT * DMAX];
+  __shared__ float sP[kFgWaves][kFgQW][KT];
+
+  const int nqb = (Sq + kFgQB - 1) / kFgQB;
+  const int bh = (int)(blockIdx.x % (unsigned)nbh);
+  const int qi = (int)(blockIdx.x / (unsigned)nbh);
+  const int qb = causal ? (nqb - 1 - qi) : qi;  // causal: heaviest query blocks first
+  const int h = bh % Hq, b = bh / Hq, hk = h / group;
+  const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
+  const int q0 = qb * kFgQB;
+  const int kk = lane % KT, qsub = lane / KT;
+
+  const typename T::S* Qb = Q + b * qsb + h * qsh;
+  const typename T::S* Kb = K + b * ksb + hk * ksh;
+  const typename T::S* Vb = V + b * vsb + hk * vsh;
+
+  for (int e = tid; e < kFgQB * DMAX; e += kFgWaves * 64) {
+    const int q = e / DMAX, d = e % DMAX;
+    sQ[e] = (q0 + q < Sq && d < D) ? T::to_f(Qb[(int64_t)(q0 + q) * qss + d]) : 0.f;
+  }
+  const int kend = causal ? min(Sk, q0 + kFgQB) : Sk;
+  const int ntiles = (kend + KT - 1) / KT;
+
+  // score of key k0 + kk for this wave's query slot qs (0 .. kFgQW - 1): the reference's roundings
+  auto score = [&](int qs, int k0) -> float {
+    const int q = q0 + w * kFgQW + qs, key = k0 + kk;
+    const float* qr = &sQ[(w * kFgQW + qs) * DMAX];
+    const float* kr = &sK[kk * KP];
+    float dot = 0.f;
+    for (int d = 0; d < D; ++d) dot = __builtin_fmaf(qr[d], kr[d], dot);
+    float sc = T::rnd(T::rnd(dot) * scale);
+    if (key >= Sk || (causal && key > q)) sc = -INFINITY;
+    return sc;
+  };
+  auto load_k = [&](int k0) {
+    for (int e = tid; e < KT * DMAX; e += kFgWaves * 64) {
+      const int r = e / DMAX, d = e % DMAX;
+      sK[r * KP + d] = (k0 + r < Sk && d < D) ? T::to_f(Kb[(int64_t)(k0 + r) * kss + d]) : 0.f;
+    }
+  };
+  auto load_v = [&](int k0) {
+    for (int e = tid; e < KT * DMAX; e += kFgWaves * 64) {
+      const int r = e / DMAX, d = e % DMAX;
+      sV[e] = (k0 + r < Sk && d < D) ? T::to_f(Vb[(int64_t)(k0 + r) * vss + d]) : 0.f;
+    }
+  };
+
+  // pass 1: row max (NaN-propagating) and sum of exp(s - max), kept identical in every lane
+  float m[kFgQW], l[kFgQW];
+#pragma unroll
+  for (int i = 0; i < kFgQW; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.f;
+  }
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();
+    load_k(t * KT);
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < kFgQW / QPP; ++g) {
+      const float sc = score(g * QPP + qsub, t * KT);
+#pragma unroll
+      for (int u = 0; u < QPP; ++u) {
+        // lanes u * KT .. u * KT + KT - 1 hold query slot g * QPP + u
+        float tm = seg_reduce<KT>(sc, OpNanMax());
+        tm = __shfl(tm, u * KT, 64);
+        const int qs = g * QPP + u;
+        const float mn = nan_max(m[qs], tm);
+        float e = (qsub == u && mn != -INFINITY) ? __builtin_amdgcn_exp2f((sc - mn) * kFaLog2e) : 0.f;
+        e = __shfl(seg_reduce<KT>(e, OpAdd()), u * KT, 64);
+        l[qs] = (mn == -INFINITY) ? 0.f : l[qs] * __builtin_amdgcn_exp2f((m[qs] - mn) * kFaLog2e) + e;
+        m[qs] = mn;
+      }
+    }
+  }
+
+  // pass 2: P = rnd(exp(s - max) / sum), O += P V
+  float acc[kFgQW][RD];
+#pragma unroll
+  for (int i = 0; i < kFgQW; ++i)
+#pragma unroll
+    for (int r = 0; r < RD; ++r) acc[i][r] = 0.f;
+  float inv[kFgQW];
+#pragma unroll
+  for (int i = 0; i < kFgQW; ++i) inv[i] = 1.0f / l[i];
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();
+    load_k(t * KT);
+    load_v(t * KT);
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < kFgQW / QPP; ++g) {
+      const int qs = g * QPP + qsub;
+      const float sc = score(qs, t * KT);
+      float mq = m[0], iq = inv[0];
+#pragma unroll
+      for (int i = 1; i < kFgQW; ++i)
+        if (i == qs) {
+          mq = m[i];
+          iq = inv[i];
+        }
+      const float pe = (sc == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((sc - mq) * kFaLog2e);
+      sP[w][qs][kk] = T::rnd(pe * iq);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int qs = 0; qs < kFgQW; ++qs) {
+      for (int j = 0; j < KT; ++j) {
+        const float pj = sP[w][qs][j];
+#pragma unroll
+        for (int r = 0; r < RD; ++r) acc[qs][r] = __builtin_fmaf(pj, sV[j * DMAX + lane + 64 * r], acc[qs][r]);
+      }
+    }
+  }
+
+  typename T::S* Ob = O + b * osb + h * osh;
+#pragma unroll
+  for (int qs = 0; qs < kFgQW; ++qs) {
+    const int q = q0 + w * kFgQW + qs;
+    if (q >= Sq) continue;
+    const bool nan_row = !(m[qs] > -INFINITY && m[qs] < INFINITY);
+#pragma unroll
+    for (int r = 0; r < RD; ++r) {
+      const int d = lane + 64 * r;
+      if (d < D) Ob[(int64_t)q * oss + d] = T::from_f(nan_row ? __builtin_nanf("") : acc[qs][r]);
+    }
+  }
+}
+
+template <typename T>
+static int launch_fa_general(const void* Q, const void* K, const void* V, void* O, int64_t B, int64_t Hq,
+                             int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, const int64_t* qs, const int64_t* ks,
+                             const int64_t* vs, const int64_t* os, int causal, float sm_scale, hipStream_t st) {
+  using S = typename T::S;
+  const int64_t nblocks = cdiv(Sq, kFgQB) * Hq * B;
+  if (nblocks > INT_MAX) return AK_EINVAL;
+#define AK_FG(DM)                                                                                           \
+  fa_general<T, DM><<<dim3((unsigned)nblocks), kFgWaves * 64, 0, st>>>(                                     \
+      (const S*)Q, (const S*)K, (const S*)V, (S*)O, (int)Hq, (int)(Hq / Hkv), (int)Sq, (int)Sk, (int)D,     \
+      qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1], os[2], causal, sm_scale, \
+      (int)(Hq * B))
+  if (D <= 64) AK_FG(64);
+  else if (D <= 128) AK_FG(128);
+  else AK_FG(256);
+#undef AK_FG
+  return record_launch();
+}
+
 template <typename T, int D>
 static int launch_fa(const void* Q, const void* K, const void* V, void* O, int64_t B, int64_t Hq,
                      int64_t Hkv, int64_t Sq, int64_t Sk, const int64_t* qs, const int64_t* ks,
@@ -799,22 +978,31 @@ extern "C" int ak_flash_attn_fwd(int dtype, const void* Q, const void* K, const 
                                  int64_t D, const int64_t* q_strides, const int64_t* k_strides,
                                  const int64_t* v_strides, const int64_t* o_strides, int causal,
                                  float sm_scale, hipStream_t stream) {
-  if (B < 0 || Hq < 0 || Hkv <= 0 || Sq < 0 || Sk < 0) return AK_EINVAL;
+  if (B < 0 || Hq < 0 || Hkv <= 0 || Sq < 0 || Sk < 0 || D <= 0) return AK_EINVAL;
   if (Hq % Hkv != 0) return AK_EINVAL;
   if (!q_strides || !k_strides || !v_strides || !o_strides) return AK_EINVAL;
+  if (dtype != AK_F32 && dtype != AK_F16 && dtype != AK_BF16) return AK_EINVAL;
+  if (D > 256) return AK_EUNSUPPORTED;
   if (B == 0 || Hq == 0 || Sq == 0) return AK_OK;
   if (!Q || !K || !V || !O) return AK_EINVAL;
   if (B * Hq > INT_MAX || Sq > INT_MAX || Sk > INT_MAX) return AK_EINVAL;
-  if (dtype != AK_F16 && dtype != AK_BF16) return AK_EUNSUPPORTED;
-  if (D != 64 && D != 128) return AK_EUNSUPPORTED;
-  // 16-byte aligned rows: every stride a multiple of 8 elements, 16-byte aligned bases
+  if (Sk == 0) return AK_EUNSUPPORTED;  // softmax over an empty key set
+  const bool c = causal != 0;
+  // The MFMA kernels: f16 / bf16, D 64 or 128, 16-byte aligned rows (every stride a multiple of 8
+  // elements, 16-byte aligned bases). Everything else runs fa_general.
+  bool fast = dtype != AK_F32 && (D == 64 || D == 128);
   const int64_t* all[4] = {q_strides, k_strides, v_strides, o_strides};
   for (int i = 0; i < 4; ++i)
     for (int j = 0; j < 3; ++j)
-      if (all[i][j] % 8 != 0) return AK_EUNSUPPORTED;
-  if (!host_aligned16(Q) || !host_aligned16(K) || !host_aligned16(V) || !host_aligned16(O)) return AK_EUNSUPPORTED;
-  if (Sk == 0) return AK_EUNSUPPORTED;  // softmax over an empty key set
-  const bool c = causal != 0;
+      if (all[i][j] % 8 != 0) fast = false;
+  if (!host_aligned16(Q) || !host_aligned16(K) || !host_aligned16(V) || !host_aligned16(O)) fast = false;
+  if (!fast) {
+    if (dtype == AK_F32)
+      return launch_fa_general<TF32>(Q, K, V, O, B, Hq, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides, o_strides, c, sm_scale, stream);
+    if (dtype == AK_F16)
+      return launch_fa_general<TF16>(Q, K, V, O, B, Hq, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides, o_strides, c, sm_scale, stream);
+    return launch_fa_general<TBF16>(Q, K, V, O, B, Hq, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides, o_strides, c, sm_scale, stream);
+  }
   if (dtype == AK_F16) {
     if (D == 64) return launch_fa<TF16, 64>(Q, K, V, O, B, Hq, Hkv, Sq, Sk, q_strides, k_strides, v_strides, o_strides, c, sm_scale, stream);
     return launch_fa<TF16, 128>(Q, K, V, O, B, Hq, Hkv, Sq, Sk, q_strides, k_strides, v_strides, o_strides, c, sm_scale, stream);

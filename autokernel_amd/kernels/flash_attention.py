@@ -4,8 +4,9 @@ Mirrors reference.py:32-42 and kernels/flash_attention.py:130: Q, K, V [batch, h
 (3-D [heads, seq, D] also accepted), default scale D**-0.5, causal mask j > i (top-left aligned).
 K / V may carry fewer heads than Q when the head count divides (grouped-query attention; one KV
 head broadcasts, as the reference's matmul does). Strided views with a contiguous last dim are
-read in place, so [B, S, H, D] tensors need no transpose copy. f16 / bf16, D in {64, 128}.
-Runs ak_flash_attn_fwd (attention.hip).
+read in place, so [B, S, H, D] tensors need no transpose copy. f16 / bf16 with D 64 or 128 run
+the MFMA kernels; fp32 and any other D up to 256 run the general kernel, with the reference's
+roundings step by step. Runs ak_flash_attn_fwd (attention.hip).
 """
 from __future__ import annotations
 
@@ -34,10 +35,10 @@ def attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, causal: bool = 
         raise ValueError(f"flash_attention: {Hq} query heads not a multiple of {Hkv} KV heads")
     if not (Q.dtype == K.dtype == V.dtype):
         raise ValueError("flash_attention: Q, K, V dtypes differ")
-    if Q.dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError(f"flash_attention: dtype {Q.dtype} unsupported (float16, bfloat16)")
-    if D not in (64, 128):
-        raise ValueError(f"flash_attention: head_dim {D} unsupported (64, 128)")
+    if Q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError(f"flash_attention: dtype {Q.dtype} unsupported (float16, bfloat16, float32)")
+    if not 1 <= D <= 256:
+        raise ValueError(f"flash_attention: head_dim {D} unsupported (1 .. 256)")
     code = _lib.dtype_code(Q, "flash_attention")
     if sm_scale is None:
         sm_scale = D ** -0.5

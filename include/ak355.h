@@ -35,7 +35,7 @@ typedef enum ak_dtype {
 typedef enum ak_status {
     AK_OK = 0,
     AK_EINVAL = 1,        /* bad argument: null pointer, negative size, bad dtype */
-    AK_EUNSUPPORTED = 2,  /* valid request this build has no kernel for (e.g. head_dim 96) */
+    AK_EUNSUPPORTED = 2,  /* valid request this build has no kernel for (e.g. head_dim 320) */
     AK_EHIP = 3           /* kernel launch failed; see ak_last_hip_error_string() */
 } ak_status;
 
@@ -212,7 +212,10 @@ int ak_mlp_gate_up(int dtype, const void* x, const void* w_gate, const void* w_u
  * Q, O: [B, Hq, Sq, D]-indexed, K, V: [B, Hkv, Sk, D]-indexed, each given by element strides
  * (batch, head, seq); the last dim is contiguous. Hq must be a multiple of Hkv (grouped-query
  * attention: query head h reads KV head h / (Hq / Hkv)). causal masks key j > query i
- * (top-left aligned, as torch.triu(ones(Sq, Sk), 1) does). D in {64, 128}. f16 / bf16.
+ * (top-left aligned, as torch.triu(ones(Sq, Sk), 1) does). f16 / bf16 with D 64 or 128 and
+ * 16-byte aligned rows run the MFMA kernels; fp32, any other D from 1 to 256 and unaligned rows run
+ * a general kernel that keeps the reference's roundings (scores and their scaled value in the
+ * element type, softmax output rounded, P V accumulated in fp32). D above 256: AK_EUNSUPPORTED.
  * Replaces: reference.py:32-42 flash_attention_ref; kernels/cuda/flash_attention.py:207-235;
  *           kernels/flash_attention.py:130 kernel_fn(Q, K, V, causal, sm_scale).
  */

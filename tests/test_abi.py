@@ -83,8 +83,9 @@ def test_invalid_arguments_rejected_on_host(lib):
     assert lib.ak_reduce_max(1, x, x, 2, 0, 1, None) == _lib.AK_EINVAL      # max of nothing
     s = _lib.i64_array([8, 8, 8])
     assert lib.ak_flash_attn_fwd(1, x, x, x, x, 1, 4, 3, 8, 8, 64, s, s, s, s, 1, 1.0, None) == _lib.AK_EINVAL
-    assert lib.ak_flash_attn_fwd(1, x, x, x, x, 1, 4, 4, 8, 8, 96, s, s, s, s, 1, 1.0, None) == _lib.AK_EUNSUPPORTED
-    assert lib.ak_flash_attn_fwd(0, x, x, x, x, 1, 4, 4, 8, 8, 64, s, s, s, s, 1, 1.0, None) == _lib.AK_EUNSUPPORTED
+    assert lib.ak_flash_attn_fwd(1, x, x, x, x, 1, 4, 4, 8, 8, 320, s, s, s, s, 1, 1.0, None) == _lib.AK_EUNSUPPORTED
+    assert lib.ak_flash_attn_fwd(7, x, x, x, x, 1, 4, 4, 8, 8, 64, s, s, s, s, 1, 1.0, None) == _lib.AK_EINVAL
+    assert lib.ak_flash_attn_fwd(0, x, x, x, x, 1, 4, 4, 8, 0, 64, s, s, s, s, 1, 1.0, None) == _lib.AK_EUNSUPPORTED
 
 
 def test_kernel_fn_refuses_cpu_tensors():

@@ -401,3 +401,51 @@ def test_copy_reference_kernel(gpu):
         _lib.check(_lib.load().ak_copy(src.data_ptr(), dst.data_ptr(), n * 2, _lib.stream_of(src)), "ak_copy")
         torch.cuda.synchronize()
         assert torch.equal(src, dst)
+
+
+@pytest.mark.parametrize("D", [16, 32, 96, 256])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_attention_general_head_dims(gpu, D, dt):
+    """Head dims the MFMA kernels do not take run the general kernel (the Triton starter's
+    D in 16..256, kernels/flash_attention.py:159), at the harness's f16 / bf16 tolerance."""
+    g = torch.Generator().manual_seed(D)
+    for causal, (B, H, S) in ((True, (1, 4, 127)), (False, (2, 2, 200))):
+        Q, K, V = (torch.randn(B, H, S, D, generator=g).to(dt) for _ in range(3))
+        out = kernels.get("flash_attention")(Q.to(gpu), K.to(gpu), V.to(gpu), causal)
+        assert_close(out, R.flash_attention_ref(Q, K, V, causal), 1e-2, 1e-2, f"D={D} {dt} causal={causal}")
+
+
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+def test_attention_fp32(gpu, D):
+    """fp32 attention at the north star's fp32 tolerance (1e-4): the general kernel keeps fp32
+    throughout, including GQA, a rectangular causal mask, an explicit scale and strided views."""
+    g = torch.Generator().manual_seed(100 + D)
+    Q = torch.randn(2, 4, 150, D, generator=g)
+    K = torch.randn(2, 2, 170, D, generator=g)
+    V = torch.randn(2, 2, 170, D, generator=g)
+    for causal in (True, False):
+        exp = R.flash_attention_ref(Q, K.repeat_interleave(2, 1), V.repeat_interleave(2, 1), causal, 0.3)
+        out = kernels.get("flash_attention")(Q.to(gpu), K.to(gpu), V.to(gpu), causal, 0.3)
+        assert_close(out, exp, 1e-4, 1e-4, f"fp32 D={D} causal={causal}")
+    # [B, S, H, D] storage read through transposed views
+    Qs = Q.transpose(1, 2).contiguous().to(gpu).transpose(1, 2)
+    Ks = K[:, :1].repeat(1, 4, 1, 1).transpose(1, 2).contiguous().to(gpu).transpose(1, 2)
+    Vs = V[:, :1].repeat(1, 4, 1, 1).transpose(1, 2).contiguous().to(gpu).transpose(1, 2)
+    exp = R.flash_attention_ref(Q, K[:, :1].repeat(1, 4, 1, 1), V[:, :1].repeat(1, 4, 1, 1), True)
+    assert_close(kernels.get("flash_attention")(Qs, Ks, Vs, True), exp, 1e-4, 1e-4, f"fp32 strided D={D}")
+
+
+def test_attention_general_overflow_rows(gpu):
+    """The general kernel rounds Q K^T and its scaled value to f16 as the reference does, so
+    scores beyond the f16 range give the reference's inf / NaN rows (the harness's mixed_scale
+    transform) at D = 32; the NaN pattern must match exactly."""
+    g = torch.Generator().manual_seed(5)
+    Q, K, V = (torch.randn(1, 2, 96, 32, generator=g).half() for _ in range(3))
+    Q[0, 0, 10:20] *= 300
+    K[0, 0, :5] *= 300
+    out = kernels.get("flash_attention")(Q.to(gpu), K.to(gpu), V.to(gpu), True).cpu()
+    exp = R.flash_attention_ref(Q, K, V, True)
+    assert torch.equal(torch.isnan(out), torch.isnan(exp))
+    assert torch.isnan(exp).any()
+    keep = ~torch.isnan(exp)
+    assert_close(out[keep], exp[keep], 1e-2, 1e-2, "finite rows")
