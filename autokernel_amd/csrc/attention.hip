@@ -772,29 +772,33 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
 // are exact in fp32). Two passes over the keys: the first takes each query row's max and sum, the
 // second forms the normalised P, rounds it as F.softmax's output is rounded, and accumulates P V.
 // A row whose max is +-inf or NaN comes out NaN, as softmax makes it.
-// Work split: a block is 4 waves and 32 queries (8 per wave) of one (batch, head). Key tiles of
+// Work split: a block is 8 waves (two per SIMD) and 64 queries (8 per wave) of one (batch, head). Key tiles of
 // KT = 64 keys (32 for head_dim above 128, so the tiles fit LDS) are staged in LDS as fp32; for the
-// scores lane L takes key L % KT of query L / KT (+ 64 / KT per step), for P V lane L owns dims
-// L, L + 64, ... K rows are padded by one float, so the 64 lanes reading one dim of 64 rows hit 64
-// banks.
+// scores lane L takes key L % KT against the wave's query slots L / KT, L / KT + 64 / KT, ..., reading
+// each 16-byte chunk of its K row once for all of them; for P V lane L owns dims L, L + 64, ... and
+// reads P four keys at a time. K rows are padded by 4 floats, so the 16-byte reads of 8 rows (one
+// LDS phase) land on 32 distinct banks.
 // ============================================================================================
-constexpr int kFgWaves = 4, kFgQW = 8, kFgQB = kFgWaves * kFgQW;
+constexpr int kFgWaves = 8, kFgQW = 8, kFgQB = kFgWaves * kFgQW;
 
 template <typename T, int DMAX>
 __global__ __launch_bounds__(kFgWaves * 64) void fa_general(
     const typename T::S* __restrict__ Q, const typename T::S* __restrict__ K,
     const typename T::S* __restrict__ V, typename T::S* __restrict__ O, int Hq, int group, int Sq, int Sk,
     int D, int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb,
-    int64_t vsh, int64_t vss, int64_t osb, int64_t osh, int64_t oss, int causal, float scale, int nbh) {
+    int64_t vsh, int64_t vss, int64_t osb, int64_t osh, int64_t oss, int causal, float scale, int nbh,
+    int vec4) {
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
   constexpr int KT = DMAX > 128 ? 32 : 64;  // LDS holds fp32: 256-wide rows take 32-key tiles
-  constexpr int QPP = 64 / KT;        // queries scored side by side in one wave
-  constexpr int KP = DMAX + 1;        // padded K row in LDS (floats)
-  constexpr int RD = DMAX / 64;       // dims per lane in P V
-  static_assert(DMAX % 64 == 0 && kFgQW % QPP == 0, "fa_general tiling");
-  __shared__ float sQ[kFgQB * DMAX];
-  __shared__ float sK[KT * KP];
-  __shared__ float sV[KT * DMAX];
-  __shared__ float sP[kFgWaves][kFgQW][KT];
+  constexpr int QPP = 64 / KT;               // queries scored side by side in one wave
+  constexpr int NQ = kFgQW / QPP;            // query slots per lane: qs = i * QPP + lane / KT
+  constexpr int KP = DMAX + 4;               // padded K row (floats): 16-byte reads conflict-free
+  constexpr int RD = DMAX / 64;              // dims per lane in P V
+  static_assert(DMAX % 64 == 0 && kFgQW % QPP == 0 && KT % 4 == 0, "fa_general tiling");
+  __shared__ __attribute__((aligned(16))) float sQ[kFgQB * DMAX];
+  __shared__ __attribute__((aligned(16))) float sK[KT * KP];
+  __shared__ __attribute__((aligned(16))) float sV[KT * DMAX];
+  __shared__ __attribute__((aligned(16))) float sP[kFgWaves][kFgQW][KT];
 
   const int nqb = (Sq + kFgQB - 1) / kFgQB;
   const int bh = (int)(blockIdx.x % (unsigned)nbh);
@@ -804,41 +808,74 @@ __global__ __launch_bounds__(kFgWaves * 64) void fa_general(
   const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
   const int q0 = qb * kFgQB;
   const int kk = lane % KT, qsub = lane / KT;
+  const int D4 = (D + 3) & ~3;  // dims read in 16-byte steps (zeros past D)
 
   const typename T::S* Qb = Q + b * qsb + h * qsh;
   const typename T::S* Kb = K + b * ksb + hk * ksh;
   const typename T::S* Vb = V + b * vsb + hk * vsh;
 
-  for (int e = tid; e < kFgQB * DMAX; e += kFgWaves * 64) {
-    const int q = e / DMAX, d = e % DMAX;
-    sQ[e] = (q0 + q < Sq && d < D) ? T::to_f(Qb[(int64_t)(q0 + q) * qss + d]) : 0.f;
-  }
+  // rows of `rows` x DMAX floats from a [*, D] matrix with row stride ld into LDS (row pitch
+  // pitch), zeros past D and past `valid` rows; vec4: D, the strides and the base are multiples of
+  // 4 elements, so 4 consecutive elements load together
+  auto stage = [&](float* dst, int pitch, const typename T::S* src, int64_t ld, int rows, int valid) {
+    if (vec4) {
+      using S = typename T::S;
+      for (int e = tid; e < rows * (DMAX / 4); e += kFgWaves * 64) {
+        const int r = e / (DMAX / 4), d = (e % (DMAX / 4)) * 4;
+        f32x4v v = {0.f, 0.f, 0.f, 0.f};
+        if (r < valid && d < D) {
+          const S* p = src + (int64_t)r * ld + d;
+          if constexpr (sizeof(S) == 4) {
+            v = *reinterpret_cast<const f32x4v*>(p);
+          } else {
+            const u32x2 h = *reinterpret_cast<const u32x2*>(p);
+            v = f32x4v{T::to_f((S)(h[0] & 0xffffu)), T::to_f((S)(h[0] >> 16)), T::to_f((S)(h[1] & 0xffffu)),
+                       T::to_f((S)(h[1] >> 16))};
+          }
+        }
+        *reinterpret_cast<f32x4v*>(dst + r * pitch + d) = v;
+      }
+    } else {
+      for (int e = tid; e < rows * DMAX; e += kFgWaves * 64) {
+        const int r = e / DMAX, d = e % DMAX;
+        dst[r * pitch + d] = (r < valid && d < D) ? T::to_f(src[(int64_t)r * ld + d]) : 0.f;
+      }
+    }
+  };
+  stage(sQ, DMAX, Qb + (int64_t)q0 * qss, qss, kFgQB, Sq - q0);
   const int kend = causal ? min(Sk, q0 + kFgQB) : Sk;
   const int ntiles = (kend + KT - 1) / KT;
 
-  // score of key k0 + kk for this wave's query slot qs (0 .. kFgQW - 1): the reference's roundings
-  auto score = [&](int qs, int k0) -> float {
-    const int q = q0 + w * kFgQW + qs, key = k0 + kk;
-    const float* qr = &sQ[(w * kFgQW + qs) * DMAX];
+  // scores of key k0 + kk against this lane's NQ query slots, with the reference's roundings;
+  // each K chunk is read once for all of them (the dot products run in d order)
+  auto scores = [&](int k0, float (&sc)[NQ]) {
+    float dot[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) dot[i] = 0.f;
     const float* kr = &sK[kk * KP];
-    float dot = 0.f;
-    for (int d = 0; d < D; ++d) dot = __builtin_fmaf(qr[d], kr[d], dot);
-    float sc = T::rnd(T::rnd(dot) * scale);
-    if (key >= Sk || (causal && key > q)) sc = -INFINITY;
-    return sc;
-  };
-  auto load_k = [&](int k0) {
-    for (int e = tid; e < KT * DMAX; e += kFgWaves * 64) {
-      const int r = e / DMAX, d = e % DMAX;
-      sK[r * KP + d] = (k0 + r < Sk && d < D) ? T::to_f(Kb[(int64_t)(k0 + r) * kss + d]) : 0.f;
+    const float* qr = &sQ[(w * kFgQW + qsub) * DMAX];
+    for (int d = 0; d < D4; d += 4) {
+      const f32x4v kv = *reinterpret_cast<const f32x4v*>(kr + d);
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) {
+        const f32x4v qv = *reinterpret_cast<const f32x4v*>(qr + i * QPP * DMAX + d);
+        dot[i] = __builtin_fmaf(qv[0], kv[0], dot[i]);
+        dot[i] = __builtin_fmaf(qv[1], kv[1], dot[i]);
+        dot[i] = __builtin_fmaf(qv[2], kv[2], dot[i]);
+        dot[i] = __builtin_fmaf(qv[3], kv[3], dot[i]);
+      }
+    }
+    const int key = k0 + kk;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int q = q0 + w * kFgQW + i * QPP + qsub;
+      float v = T::rnd(T::rnd(dot[i]) * scale);
+      if (key >= Sk || (causal && key > q)) v = -INFINITY;
+      sc[i] = v;
     }
   };
-  auto load_v = [&](int k0) {
-    for (int e = tid; e < KT * DMAX; e += kFgWaves * 64) {
-      const int r = e / DMAX, d = e % DMAX;
-      sV[e] = (k0 + r < Sk && d < D) ? T::to_f(Vb[(int64_t)(k0 + r) * vss + d]) : 0.f;
-    }
-  };
+  auto load_k = [&](int k0) { stage(sK, KP, Kb + (int64_t)k0 * kss, kss, KT, Sk - k0); };
+  auto load_v = [&](int k0) { stage(sV, DMAX, Vb + (int64_t)k0 * vss, vss, KT, Sk - k0); };
 
   // pass 1: row max (NaN-propagating) and sum of exp(s - max), kept identical in every lane
   float m[kFgQW], l[kFgQW];
@@ -851,22 +888,21 @@ __global__ __launch_bounds__(kFgWaves * 64) void fa_general(
     __syncthreads();
     load_k(t * KT);
     __syncthreads();
+    float sc[NQ];
+    scores(t * KT, sc);
 #pragma unroll
-    for (int g = 0; g < kFgQW / QPP; ++g) {
-      const float sc = score(g * QPP + qsub, t * KT);
+    for (int i = 0; i < NQ; ++i)
 #pragma unroll
       for (int u = 0; u < QPP; ++u) {
-        // lanes u * KT .. u * KT + KT - 1 hold query slot g * QPP + u
-        float tm = seg_reduce<KT>(sc, OpNanMax());
-        tm = __shfl(tm, u * KT, 64);
-        const int qs = g * QPP + u;
+        // lanes u * KT .. u * KT + KT - 1 hold query slot i * QPP + u
+        const int qs = i * QPP + u;
+        const float tm = __shfl(seg_reduce<KT>(sc[i], OpNanMax()), u * KT, 64);
         const float mn = nan_max(m[qs], tm);
-        float e = (qsub == u && mn != -INFINITY) ? __builtin_amdgcn_exp2f((sc - mn) * kFaLog2e) : 0.f;
+        float e = (qsub == u && mn != -INFINITY) ? __builtin_amdgcn_exp2f((sc[i] - mn) * kFaLog2e) : 0.f;
         e = __shfl(seg_reduce<KT>(e, OpAdd()), u * KT, 64);
         l[qs] = (mn == -INFINITY) ? 0.f : l[qs] * __builtin_amdgcn_exp2f((m[qs] - mn) * kFaLog2e) + e;
         m[qs] = mn;
       }
-    }
   }
 
   // pass 2: P = rnd(exp(s - max) / sum), O += P V
@@ -875,35 +911,40 @@ __global__ __launch_bounds__(kFgWaves * 64) void fa_general(
   for (int i = 0; i < kFgQW; ++i)
 #pragma unroll
     for (int r = 0; r < RD; ++r) acc[i][r] = 0.f;
-  float inv[kFgQW];
-#pragma unroll
-  for (int i = 0; i < kFgQW; ++i) inv[i] = 1.0f / l[i];
   for (int t = 0; t < ntiles; ++t) {
     __syncthreads();
     load_k(t * KT);
     load_v(t * KT);
     __syncthreads();
+    float sc[NQ];
+    scores(t * KT, sc);
 #pragma unroll
-    for (int g = 0; g < kFgQW / QPP; ++g) {
-      const int qs = g * QPP + qsub;
-      const float sc = score(qs, t * KT);
-      float mq = m[0], iq = inv[0];
+    for (int i = 0; i < NQ; ++i) {
+      // this lane's slot i * QPP + qsub: pick its statistics (qsub is 0 when QPP == 1)
+      float mq = m[i * QPP], lq = l[i * QPP];
 #pragma unroll
-      for (int i = 1; i < kFgQW; ++i)
-        if (i == qs) {
-          mq = m[i];
-          iq = inv[i];
+      for (int u = 1; u < QPP; ++u)
+        if (qsub == u) {
+          mq = m[i * QPP + u];
+          lq = l[i * QPP + u];
         }
-      const float pe = (sc == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((sc - mq) * kFaLog2e);
-      sP[w][qs][kk] = T::rnd(pe * iq);
+      const float pe = (sc[i] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((sc[i] - mq) * kFaLog2e);
+      sP[w][i * QPP + qsub][kk] = T::rnd(pe / lq);
     }
     __syncthreads();
+    for (int j = 0; j < KT; j += 4) {
+      float vv[4][RD];
 #pragma unroll
-    for (int qs = 0; qs < kFgQW; ++qs) {
-      for (int j = 0; j < KT; ++j) {
-        const float pj = sP[w][qs][j];
+      for (int t4 = 0; t4 < 4; ++t4)
 #pragma unroll
-        for (int r = 0; r < RD; ++r) acc[qs][r] = __builtin_fmaf(pj, sV[j * DMAX + lane + 64 * r], acc[qs][r]);
+        for (int r = 0; r < RD; ++r) vv[t4][r] = sV[(j + t4) * DMAX + lane + 64 * r];
+#pragma unroll
+      for (int qs = 0; qs < kFgQW; ++qs) {
+        const f32x4v pj = *reinterpret_cast<const f32x4v*>(&sP[w][qs][j]);
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+          for (int r = 0; r < RD; ++r) acc[qs][r] = __builtin_fmaf(pj[t4], vv[t4][r], acc[qs][r]);
       }
     }
   }
@@ -929,11 +970,19 @@ static int launch_fa_general(const void* Q, const void* K, const void* V, void* 
   using S = typename T::S;
   const int64_t nblocks = cdiv(Sq, kFgQB) * Hq * B;
   if (nblocks > INT_MAX) return AK_EINVAL;
+  // 4-element loads: D and every row / head / batch stride multiples of 4, bases aligned to 4 elements
+  int vec4 = D % 4 == 0;
+  const int64_t* all[3] = {qs, ks, vs};
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j)
+      if (all[i][j] % 4 != 0) vec4 = 0;
+  const uintptr_t al = 4 * sizeof(S) - 1;
+  if ((((uintptr_t)Q) | ((uintptr_t)K) | ((uintptr_t)V)) & al) vec4 = 0;
 #define AK_FG(DM)                                                                                           \
   fa_general<T, DM><<<dim3((unsigned)nblocks), kFgWaves * 64, 0, st>>>(                                     \
       (const S*)Q, (const S*)K, (const S*)V, (S*)O, (int)Hq, (int)(Hq / Hkv), (int)Sq, (int)Sk, (int)D,     \
       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1], os[2], causal, sm_scale, \
-      (int)(Hq * B))
+      (int)(Hq * B), vec4)
   if (D <= 64) AK_FG(64);
   else if (D <= 128) AK_FG(128);
   else AK_FG(256);

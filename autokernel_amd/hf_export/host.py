@@ -250,15 +250,20 @@ def flash_attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, causal: b
         raise ValueError(f"flash_attention: shapes Q{tuple(Q.shape)} K{tuple(K.shape)} V{tuple(V.shape)}")
     if Hkv == 0 or Hq % Hkv:
         raise ValueError(f"flash_attention: {Hq} query heads not a multiple of {Hkv} KV heads")
-    if not (Q.dtype == K.dtype == V.dtype) or Q.dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError("flash_attention: Q, K, V must share a float16 or bfloat16 dtype")
-    if D not in (64, 128):
-        raise ValueError(f"flash_attention: head_dim {D} unsupported (64, 128)")
+    if not (Q.dtype == K.dtype == V.dtype) or Q.dtype not in _DTYPES:
+        raise ValueError("flash_attention: Q, K, V must share a float32, float16 or bfloat16 dtype")
+    if not 1 <= D <= 256:
+        raise ValueError(f"flash_attention: head_dim {D} unsupported (1 .. 256)")
     if Sk == 0:
         raise ValueError("flash_attention: empty key sequence")
+    scale = float(D ** -0.5 if sm_scale is None else sm_scale)
+    if Q.dtype != torch.float32 and D < 128 and D != 64:
+        # narrow f16 / bf16 heads: zero-padded to 64 / 128 onto the MFMA kernels, padding dropped
+        Dp = 64 if D < 64 else 128
+        padded = [torch.nn.functional.pad(t, (0, Dp - D)) for t in (Q, K, V)]
+        return flash_attention(*padded, causal, scale)[..., :D].contiguous()
     O = torch.empty((B, Hq, Sq, D), device=Q.device, dtype=Q.dtype)
-    ops.flash_attn_fwd(O, _attn_operand(Q), _attn_operand(K), _attn_operand(V), bool(causal),
-                       float(D ** -0.5 if sm_scale is None else sm_scale))
+    ops.flash_attn_fwd(O, _attn_operand(Q), _attn_operand(K), _attn_operand(V), bool(causal), scale)
     return O
 
 

@@ -5,8 +5,10 @@ Mirrors reference.py:32-42 and kernels/flash_attention.py:130: Q, K, V [batch, h
 K / V may carry fewer heads than Q when the head count divides (grouped-query attention; one KV
 head broadcasts, as the reference's matmul does). Strided views with a contiguous last dim are
 read in place, so [B, S, H, D] tensors need no transpose copy. f16 / bf16 with D 64 or 128 run
-the MFMA kernels; fp32 and any other D up to 256 run the general kernel, with the reference's
-roundings step by step. Runs ak_flash_attn_fwd (attention.hip).
+the MFMA kernels, and so do f16 / bf16 heads narrower than 128 (16, 32, 96, ...), zero-padded to
+64 or 128: zero columns add nothing to Q K^T, the padded output columns are dropped, and the scale
+stays D**-0.5 of the true D. fp32, and f16 / bf16 heads wider than 128, run the general kernel, which
+keeps the reference's roundings step by step. Runs ak_flash_attn_fwd (attention.hip).
 """
 from __future__ import annotations
 
@@ -42,6 +44,14 @@ def attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, causal: bool = 
     code = _lib.dtype_code(Q, "flash_attention")
     if sm_scale is None:
         sm_scale = D ** -0.5
+    if Q.dtype != torch.float32 and D < 128 and D != 64:
+        Dp = 64 if D < 64 else 128
+        padded = [torch.nn.functional.pad(t, (0, Dp - D)) for t in (Q, K, V)]
+        res = attention(*padded, causal, sm_scale)[..., :D]
+        if out is None:
+            return res.contiguous()
+        out.copy_(res)
+        return out
     Q, K, V = _prep(Q), _prep(K), _prep(V)
     O = out if out is not None else torch.empty((B, Hq, Sq, D), device=Q.device, dtype=Q.dtype)
     if Sk == 0:

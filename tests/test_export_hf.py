@@ -163,6 +163,10 @@ def test_exported_layouts_match_kernels(gpu):
     k = torch.randn(2, 200, 2, 128, generator=g).half().to(gpu).transpose(1, 2)
     v = torch.randn(2, 200, 2, 128, generator=g).half().to(gpu).transpose(1, 2)
     assert torch.equal(host.flash_attention(q, k, v, True), kernels.get("flash_attention")(q, k, v, True))
+    q, k, v = (torch.randn(1, 4, 90, 96, generator=g).to(gpu) for _ in range(3))  # fp32, D 96: general kernel
+    assert torch.equal(host.flash_attention(q, k, v, False), kernels.get("flash_attention")(q, k, v, False))
+    q, k, v = (t.half() for t in (q, k, v))  # f16, D 96: zero-padded onto the MFMA kernel
+    assert torch.equal(host.flash_attention(q, k, v, True), kernels.get("flash_attention")(q, k, v, True))
     t = torch.randn(6, 70, 33, generator=g).half().to(gpu)
     for d in (0, 1, -1):
         assert torch.equal(host.reduce(t, d), kernels.get("reduce")(t, d))

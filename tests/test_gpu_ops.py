@@ -403,16 +403,34 @@ def test_copy_reference_kernel(gpu):
         assert torch.equal(src, dst)
 
 
+def _attention_abi(Q, K, V, causal, scale=None):
+    """ak_flash_attn_fwd called directly (no padding in Python): for f16 / bf16 heads other than 64
+    and 128 this is the general kernel."""
+    from autokernel_amd import _lib
+    B, H, S, D = Q.shape
+    O = torch.empty_like(Q)
+    a = [_lib.i64_array(t.stride()[:3]) for t in (Q, K, V, O)]
+    st = _lib.load().ak_flash_attn_fwd(_lib.dtype_code(Q, "fa"), Q.data_ptr(), K.data_ptr(), V.data_ptr(),
+                                       O.data_ptr(), B, H, K.shape[1], S, K.shape[2], D, a[0], a[1], a[2], a[3],
+                                       int(causal), D ** -0.5 if scale is None else scale, _lib.stream_of(Q))
+    _lib.check(st, "ak_flash_attn_fwd")
+    return O
+
+
 @pytest.mark.parametrize("D", [16, 32, 96, 256])
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
 def test_attention_general_head_dims(gpu, D, dt):
-    """Head dims the MFMA kernels do not take run the general kernel (the Triton starter's
-    D in 16..256, kernels/flash_attention.py:159), at the harness's f16 / bf16 tolerance."""
+    """Head dims other than 64 / 128 (the Triton starter's D in 16..256, kernels/flash_attention.py:159)
+    at the harness's f16 / bf16 tolerance, both through kernel_fn (narrow heads zero-padded onto the
+    MFMA kernels) and through the C ABI directly (the general kernel)."""
     g = torch.Generator().manual_seed(D)
     for causal, (B, H, S) in ((True, (1, 4, 127)), (False, (2, 2, 200))):
         Q, K, V = (torch.randn(B, H, S, D, generator=g).to(dt) for _ in range(3))
+        exp = R.flash_attention_ref(Q, K, V, causal)
         out = kernels.get("flash_attention")(Q.to(gpu), K.to(gpu), V.to(gpu), causal)
-        assert_close(out, R.flash_attention_ref(Q, K, V, causal), 1e-2, 1e-2, f"D={D} {dt} causal={causal}")
+        assert_close(out, exp, 1e-2, 1e-2, f"D={D} {dt} causal={causal}")
+        direct = _attention_abi(Q.to(gpu), K.to(gpu), V.to(gpu), causal)
+        assert_close(direct, exp, 1e-2, 1e-2, f"D={D} {dt} causal={causal} (general kernel)")
 
 
 @pytest.mark.parametrize("D", [32, 64, 128, 256])
@@ -436,16 +454,17 @@ def test_attention_fp32(gpu, D):
 
 
 def test_attention_general_overflow_rows(gpu):
-    """The general kernel rounds Q K^T and its scaled value to f16 as the reference does, so
-    scores beyond the f16 range give the reference's inf / NaN rows (the harness's mixed_scale
-    transform) at D = 32; the NaN pattern must match exactly."""
+    """Scores beyond the f16 range give the reference's inf / NaN rows (the harness's mixed_scale
+    transform) at D = 32, in the general kernel (which rounds Q K^T and its scaled value to f16 as
+    the reference does) and on the padded MFMA route; the NaN pattern must match exactly."""
     g = torch.Generator().manual_seed(5)
     Q, K, V = (torch.randn(1, 2, 96, 32, generator=g).half() for _ in range(3))
     Q[0, 0, 10:20] *= 300
     K[0, 0, :5] *= 300
-    out = kernels.get("flash_attention")(Q.to(gpu), K.to(gpu), V.to(gpu), True).cpu()
     exp = R.flash_attention_ref(Q, K, V, True)
-    assert torch.equal(torch.isnan(out), torch.isnan(exp))
     assert torch.isnan(exp).any()
     keep = ~torch.isnan(exp)
-    assert_close(out[keep], exp[keep], 1e-2, 1e-2, "finite rows")
+    for out in (_attention_abi(Q.to(gpu), K.to(gpu), V.to(gpu), True).cpu(),
+                kernels.get("flash_attention")(Q.to(gpu), K.to(gpu), V.to(gpu), True).cpu()):
+        assert torch.equal(torch.isnan(out), torch.isnan(exp))
+        assert_close(out[keep], exp[keep], 1e-2, 1e-2, "finite rows")
