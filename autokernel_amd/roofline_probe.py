@@ -79,9 +79,9 @@ PEAK_TFLOPS = 2516.6
 # (kernel-name fragment, label, flops per launch, the call that launches it); each probe runs
 # three times in this order, so dispatches are assigned to probes by order and name
 MFMA_PROBES = [
-    ("gemm_dma<ak::TBF16, 256, 256, 2, 4, 1, 0, 64, 2, true>", "matmul bf16 4096^3 (NN: [K, N] B, LDS-DMA)",
+    ("gemm_dma<ak::TBF16, 256, 256, 2, 4, 1, 0, 64, 2, true", "matmul bf16 4096^3 (NN: [K, N] B, LDS-DMA)",
      2 * 4096 ** 3, "matmul4k"),
-    ("gemm_dma<ak::TBF16, 256, 256, 2, 4, 1, 0, 64, 2, false>", "matmul bf16 8192^3 (NT: nn.Linear B, LDS-DMA)",
+    ("gemm_dma<ak::TBF16, 256, 256, 2, 4, 1, 0, 64, 2, false", "matmul bf16 8192^3 (NT: nn.Linear B, LDS-DMA)",
      2 * 8192 ** 3, "matmul8k"),
     ("gemm_dma<ak::TBF16, 256, 128, 2, 4, 2, 1", "fused_mlp gate/up bf16 2048x4096 H=11008",
      2 * 2048 * 4096 * 11008 * 2, "mlp"),
