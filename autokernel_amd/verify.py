@@ -19,7 +19,8 @@ rotary embedding, attention and the SwiGLU MLP are added here):
                     in the epilogue of the fused QKV GEMM (ak_gemm_rope)
   flash_attention   attention modules (wq / wk / wv / wo, n_heads, n_kv_heads) -> GQA-native
                     ak_flash_attn_fwd on strided [B, T, H, D] views (no repeat_interleave, no
-                    transpose copies)
+                    transpose copies); encoder attention (query / key / value / out_proj,
+                    num_heads: BERT) -> the non-causal kernel when no attention_mask is given
   fused_mlp         SwiGLU feed-forward modules (w1 gate, w3 up, w2 down) -> ak_mlp_gate_up + ak_gemm
   (with matmul)     pre-norm blocks (attention, feed_forward, attention_norm, ffn_norm) whose
                     attention and feed-forward are swapped: each residual add runs in the epilogue
@@ -228,6 +229,35 @@ class AttentionWrapper(nn.Module):
         return residual + self._proj(o.wo, y)
 
 
+class EncoderAttentionWrapper(nn.Module):
+    """Bidirectional self-attention with separate query / key / value / out_proj Linears and
+    num_heads (the reference's BERT, models/bert_base.py:16-40): the projections through ak_gemm when
+    matmul is swapped, attention through the non-causal flash-attention kernel on strided
+    [B, T, H, D] views. A call with an attention_mask goes to the original module (the kernel takes
+    no arbitrary mask)."""
+
+    def __init__(self, original: nn.Module, use_matmul: bool):
+        super().__init__()
+        self.original = original
+        self.use_matmul = use_matmul
+
+    def forward(self, x, attention_mask=None):
+        o = self.original
+        if attention_mask is not None:
+            return o(x, attention_mask)
+        B, T, C = x.shape
+        H = o.num_heads
+        D = C // H
+
+        def proj(lin, t):
+            return _linear(t, lin.weight, lin.bias) if self.use_matmul else lin(t)
+        q, k, v = (proj(lin, x).view(B, T, H, D) for lin in (o.query, o.key, o.value))
+        y = fa_mod.attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), False, None)
+        y = y.transpose(1, 2).reshape(B, T, C)
+        out = proj(o.out_proj, y)
+        return o.dropout(out) if isinstance(getattr(o, "dropout", None), nn.Module) else out
+
+
 class ResidualBlockWrapper(nn.Module):
     """Pre-norm block x = x + attention(attention_norm(x)); x = x + feed_forward(ffn_norm(x))
     (models/llama_7b.py:109-112) whose attention and feed-forward are libak355 wrappers: each
@@ -258,6 +288,11 @@ def _is_rmsnorm(m: nn.Module) -> bool:
 
 def _is_attention(m: nn.Module) -> bool:
     return all(hasattr(m, a) for a in ("wq", "wk", "wv", "wo", "n_heads", "n_kv_heads", "head_dim"))
+
+
+def _is_encoder_attention(m: nn.Module) -> bool:
+    return (all(isinstance(getattr(m, a, None), nn.Linear) for a in ("query", "key", "value", "out_proj"))
+            and isinstance(getattr(m, "num_heads", None), int))
 
 
 def _swiglu_parts(m: nn.Module):
@@ -300,6 +335,10 @@ class OptimizedModelContext:
                 continue
             if _is_attention(m) and (k & {"rotary_embedding", "flash_attention"}):
                 self._set(name, AttentionWrapper(m, "rotary_embedding" in k, "flash_attention" in k, "matmul" in k))
+                taken.update(n for n, _ in m.named_modules(prefix=name))
+                self._count("attention")
+            elif _is_encoder_attention(m) and "flash_attention" in k:
+                self._set(name, EncoderAttentionWrapper(m, "matmul" in k))
                 taken.update(n for n, _ in m.named_modules(prefix=name))
                 self._count("attention")
             elif "fused_mlp" in k and _swiglu_parts(m) is not None and not isinstance(m, nn.Linear):

@@ -102,3 +102,56 @@ def test_model_form_norm_and_strided_rope(gpu):
     eq, _ = llama.apply_rotary_emb(q, q, cos, sin)
     oq = apply_fp32_tables(qkv.to(gpu)[..., :512].view(2, 50, 8, 64), cos.to(gpu), sin.to(gpu)).cpu()
     assert (oq.float() - eq.float()).abs().max().item() <= 1e-3
+
+
+class _BertAttention(torch.nn.Module):
+    """Bidirectional self-attention shaped like the reference's BERT (models/bert_base.py:16-40)."""
+
+    def __init__(self, dim, heads):
+        super().__init__()
+        self.num_heads = heads
+        self.query, self.key, self.value, self.out_proj = (torch.nn.Linear(dim, dim) for _ in range(4))
+        self.dropout = torch.nn.Dropout(0.0)
+
+    def forward(self, x, attention_mask=None):
+        B, T, C = x.shape
+        q, k, v = (lin(x).view(B, T, self.num_heads, C // self.num_heads).transpose(1, 2)
+                   for lin in (self.query, self.key, self.value))
+        # reference attention in fp32 (stock f16 SDPA is not the comparison here)
+        y = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float(),
+                                                             attn_mask=attention_mask).to(x.dtype)
+        return self.dropout(self.out_proj(y.transpose(1, 2).reshape(B, T, C)))
+
+
+class _BertLayer(torch.nn.Module):
+    def __init__(self, dim, heads):
+        super().__init__()
+        self.attention, self.norm1 = _BertAttention(dim, heads), torch.nn.LayerNorm(dim)
+        self.mlp = torch.nn.Sequential(torch.nn.Linear(dim, 4 * dim), torch.nn.GELU(), torch.nn.Linear(4 * dim, dim))
+        self.norm2 = torch.nn.LayerNorm(dim)
+
+    def forward(self, x):
+        x = self.norm1(x + self.attention(x))
+        return self.norm2(x + self.mlp(x))
+
+
+def test_bert_shaped_encoder_all_ops(gpu):
+    """A post-LayerNorm encoder with BERT's attention module: Linear, LayerNorm and the non-causal
+    attention all run on libak355 and the output stays within the f16 tolerance of stock."""
+    torch.manual_seed(0)
+    with torch.device(gpu):
+        m = torch.nn.Sequential(*[_BertLayer(256, 4) for _ in range(2)]).half().eval()
+        x = torch.randn(2, 130, 256).half()
+    with torch.no_grad():
+        ref = m(x)
+        ctx = verify.OptimizedModelContext(m, verify.ALL_KERNELS)
+        with ctx as pm:
+            out = pm(x)
+            masked_in = torch.randn(1, 20, 256, device=gpu).half()
+            mask = torch.ones(20, 20, device=gpu, dtype=torch.bool).tril()
+            via_wrapper = pm[0].attention(masked_in, mask)  # a mask goes to the original module
+        direct = m[0].attention(masked_in, mask)
+    assert ctx.applied == {"attention": 2, "matmul": 4, "layernorm": 4}, ctx.applied
+    assert torch.equal(via_wrapper, direct)
+    c = verify.compare_outputs(ref, out, torch.float16, 1e-2, 1e-2)
+    assert c["correctness"] == "PASS", c

@@ -57,3 +57,46 @@ def test_compare_outputs_rules():
     assert verify.compare_outputs(a, b, torch.float32)["correctness"] == "FAIL"
     assert verify.compare_outputs(b, b.clone(), torch.float32)["correctness"] == "PASS"  # NaN in both
     assert verify.compare_outputs(a, a + 1, torch.float32, 1e-2, 1e-2)["correctness"] == "FAIL"
+
+
+class _EncoderAttention(nn.Module):
+    """BERT-shaped self-attention (separate query / key / value / out_proj, no mask by default)."""
+
+    def __init__(self, dim, heads):
+        super().__init__()
+        self.num_heads, self.head_dim = heads, dim // heads
+        self.query, self.key, self.value, self.out_proj = (nn.Linear(dim, dim) for _ in range(4))
+        self.dropout = nn.Dropout(0.0)
+
+    def forward(self, x, attention_mask=None):
+        import torch.nn.functional as F
+        B, T, C = x.shape
+        q, k, v = (lin(x).view(B, T, self.num_heads, self.head_dim).transpose(1, 2)
+                   for lin in (self.query, self.key, self.value))
+        y = F.scaled_dot_product_attention(q, k, v, attn_mask=attention_mask)
+        return self.dropout(self.out_proj(y.transpose(1, 2).reshape(B, T, C)))
+
+
+class _EncoderLayer(nn.Module):
+    """Post-LayerNorm encoder layer (x = norm(x + sublayer(x))): no pre-norm residual fusion applies."""
+
+    def __init__(self, dim, heads):
+        super().__init__()
+        self.attention, self.norm1 = _EncoderAttention(dim, heads), nn.LayerNorm(dim)
+        self.mlp = nn.Sequential(nn.Linear(dim, 4 * dim), nn.GELU(), nn.Linear(4 * dim, dim))
+        self.norm2 = nn.LayerNorm(dim)
+
+    def forward(self, x):
+        x = self.norm1(x + self.attention(x))
+        return self.norm2(x + self.mlp(x))
+
+
+def test_encoder_attention_strategy_applies_and_restores():
+    m = nn.Sequential(_EncoderLayer(64, 4), _EncoderLayer(64, 4))
+    before = {n: type(x) for n, x in m.named_modules()}
+    ctx = verify.OptimizedModelContext(m, verify.ALL_KERNELS)
+    with ctx:
+        assert ctx.applied == {"attention": 2, "matmul": 4, "layernorm": 4}, ctx.applied
+        assert isinstance(m[0].attention, verify.EncoderAttentionWrapper)
+        assert isinstance(m[1].mlp[0], verify.LinearWrapper)
+    assert {n: type(x) for n, x in m.named_modules()} == before
