@@ -468,3 +468,4 @@ def test_attention_general_overflow_rows(gpu):
                 kernels.get("flash_attention")(Q.to(gpu), K.to(gpu), V.to(gpu), True).cpu()):
         assert torch.equal(torch.isnan(out), torch.isnan(exp))
         assert_close(out[keep], exp[keep], 1e-2, 1e-2, "finite rows")
+
