@@ -469,3 +469,78 @@ def test_attention_general_overflow_rows(gpu):
         assert torch.equal(torch.isnan(out), torch.isnan(exp))
         assert_close(out[keep], exp[keep], 1e-2, 1e-2, "finite rows")
 
+
+# ------------------------------------------------------------------ randomized shape sweeps
+def _rand_shapes(seed, n, lo, hi, align_choices):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        dims = []
+        for a in align_choices:
+            v = int(rng.integers(lo, hi))
+            dims.append(max(a, v - v % a))
+        out.append(tuple(dims))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K", _rand_shapes(7, 10, 1, 700, (1, 4, 1)) + _rand_shapes(8, 6, 64, 1600, (16, 8, 64)))
+def test_gemm_epilogues_random_shapes(gpu, M, N, K):
+    """Seeded random shapes across the LDS-DMA path (K % 64 == 0), the register-staged fallback
+    and ragged tile edges: plain, residual and rotary epilogues in f16 and bf16, both B layouts;
+    the epilogue variants equal the plain GEMM followed by the separate op, bit for bit."""
+    from autokernel_amd import llama
+    from autokernel_amd.kernels.matmul import gemm, gemm_residual, gemm_rope
+    g = torch.Generator().manual_seed(M * 1009 + N * 31 + K)
+    for dt in (torch.float16, torch.bfloat16):
+        A = (torch.randn(M, K, generator=g) / max(K, 1) ** 0.5).to(dt)
+        W = torch.randn(N, K, generator=g).to(dt)
+        Rr = torch.randn(M, N, generator=g).to(dt)
+        Ad, Rd = A.to(gpu), Rr.to(gpu)
+        for bt in (True, False):
+            Bd = W.to(gpu).t() if bt else W.t().contiguous().to(gpu)
+            plain = gemm(Ad, Bd)
+            assert_close(plain, R.matmul_ref(A.float(), W.float().T).to(dt), 2e-2, 2e-2, f"{M}x{N}x{K} bt={bt} {dt}")
+            assert torch.equal(gemm_residual(Ad, Bd, Rd), Rd + plain), f"residual {M}x{N}x{K} bt={bt} {dt}"
+            if N % 8 == 0:
+                D = 8 if N % 16 else 16
+                T = max(1, M // 2) if M % 2 == 0 else M
+                cos, sin = (t.to(gpu) for t in llama.rope_tables(D, T))
+                rot = (N // D - (1 if N // D > 1 else 0)) * D
+                out = gemm_rope(Ad, Bd, cos, sin, T, D, rot)
+                ref = plain.clone()
+                if rot:
+                    view = plain[:, :rot].reshape(M // T, T, rot // D, D)
+                    eq, _ = llama.apply_rotary_emb(view, view, cos, sin)
+                    ref[:, :rot] = eq.reshape(M, rot)
+                assert torch.equal(out, ref), f"rope {M}x{N}x{K} bt={bt} {dt} D={D}"
+
+
+def _attn_cases():
+    rng = np.random.default_rng(11)
+    cases = []
+    for _ in range(12):
+        B = int(rng.integers(1, 3))
+        Hk = int(rng.integers(1, 3))
+        Hq = Hk * int(rng.choice([1, 2, 4]))
+        Sq, Sk = int(rng.integers(1, 300)), int(rng.integers(1, 300))
+        D = int(rng.choice([16, 24, 32, 40, 64, 80, 96, 128, 160, 256]))
+        dt = [torch.float16, torch.bfloat16, torch.float32][int(rng.integers(0, 3))]
+        causal = bool(rng.integers(0, 2))
+        cases.append(pytest.param(B, Hq, Hk, Sq, Sk, D, dt, causal, id=f"{B}x{Hq}/{Hk}x{Sq}x{Sk}x{D}-{str(dt)[6:]}-{'c' if causal else 'n'}"))
+    return cases
+
+
+@pytest.mark.parametrize("B,Hq,Hk,Sq,Sk,D,dt,causal", _attn_cases())
+def test_attention_random_shapes(gpu, B, Hq, Hk, Sq, Sk, D, dt, causal):
+    """Seeded random attention problems over every path (MFMA kernels, zero-padded narrow heads,
+    the general kernel): GQA, rectangular causal masks, ragged lengths, f16 / bf16 / fp32."""
+    g = torch.Generator().manual_seed(B * 7 + Hq * 13 + Sq * 17 + Sk * 19 + D)
+    Q = torch.randn(B, Hq, Sq, D, generator=g).to(dt)
+    K = torch.randn(B, Hk, Sk, D, generator=g).to(dt)
+    V = torch.randn(B, Hk, Sk, D, generator=g).to(dt)
+    rep = Hq // Hk
+    exp = R.flash_attention_ref(Q, K.repeat_interleave(rep, 1), V.repeat_interleave(rep, 1), causal)
+    out = kernels.get("flash_attention")(Q.to(gpu), K.to(gpu), V.to(gpu), causal)
+    tol = 1e-4 if dt == torch.float32 else 1e-2
+    # top-left causal mask: query i always sees key 0, so no row is empty
+    assert_close(out, exp, tol, tol, f"attention {B}x{Hq}/{Hk}x{Sq}x{Sk}x{D} {dt} causal={causal}")
