@@ -20,7 +20,9 @@ rotary embedding, attention and the SwiGLU MLP are added here):
   flash_attention   attention modules (wq / wk / wv / wo, n_heads, n_kv_heads) -> GQA-native
                     ak_flash_attn_fwd on strided [B, T, H, D] views (no repeat_interleave, no
                     transpose copies); encoder attention (query / key / value / out_proj,
-                    num_heads: BERT) -> the non-causal kernel when no attention_mask is given
+                    num_heads: BERT) -> the non-causal kernel when no attention_mask is given;
+                    fused-QKV causal attention (c_attn / c_proj, n_head, a tril mask: GPT-2)
+                    -> the causal kernel on column slices of the c_attn output
   fused_mlp         SwiGLU feed-forward modules (w1 gate, w3 up, w2 down) -> ak_mlp_gate_up + ak_gemm
   (with matmul)     pre-norm blocks (attention, feed_forward, attention_norm, ffn_norm) whose
                     attention and feed-forward are swapped: each residual add runs in the epilogue
@@ -258,6 +260,33 @@ class EncoderAttentionWrapper(nn.Module):
         return o.dropout(out) if isinstance(getattr(o, "dropout", None), nn.Module) else out
 
 
+class FusedQKVAttentionWrapper(nn.Module):
+    """Causal self-attention with one fused c_attn Linear (3 * n_embd outputs) and a lower-triangular
+    mask buffer (the reference's GPT-2, models/gpt2.py:18-54): c_attn and c_proj through ak_gemm when
+    matmul is swapped; q, k and v read in place as column slices of the c_attn output by the causal
+    flash-attention kernel (no split copies, no materialised T x T scores)."""
+
+    def __init__(self, original: nn.Module, use_matmul: bool):
+        super().__init__()
+        self.original = original
+        self.use_matmul = use_matmul
+
+    def forward(self, x):
+        o = self.original
+        B, T, C = x.shape
+        H = o.n_head
+        D = C // H
+
+        def proj(lin, t):
+            return _linear(t, lin.weight, lin.bias) if self.use_matmul else lin(t)
+        qkv = proj(o.c_attn, x)
+        q, k, v = (qkv[..., i * C:(i + 1) * C].view(B, T, H, D).transpose(1, 2) for i in range(3))
+        y = fa_mod.attention(q, k, v, True, None).transpose(1, 2).reshape(B, T, C)
+        out = proj(o.c_proj, y)
+        drop = getattr(o, "resid_dropout", None)
+        return drop(out) if isinstance(drop, nn.Module) else out
+
+
 class ResidualBlockWrapper(nn.Module):
     """Pre-norm block x = x + attention(attention_norm(x)); x = x + feed_forward(ffn_norm(x))
     (models/llama_7b.py:109-112) whose attention and feed-forward are libak355 wrappers: each
@@ -288,6 +317,20 @@ def _is_rmsnorm(m: nn.Module) -> bool:
 
 def _is_attention(m: nn.Module) -> bool:
     return all(hasattr(m, a) for a in ("wq", "wk", "wv", "wo", "n_heads", "n_kv_heads", "head_dim"))
+
+
+def _is_fused_qkv_causal_attention(m: nn.Module) -> bool:
+    """c_attn [3 C, C] / c_proj Linears, n_head, n_embd and a causal (lower-triangular ones) mask."""
+    c_attn, c_proj = getattr(m, "c_attn", None), getattr(m, "c_proj", None)
+    n_head, n_embd = getattr(m, "n_head", None), getattr(m, "n_embd", None)
+    mask = getattr(m, "bias", None)
+    if not (isinstance(c_attn, nn.Linear) and isinstance(c_proj, nn.Linear) and isinstance(n_head, int)
+            and isinstance(n_embd, int) and isinstance(mask, torch.Tensor) and mask.dim() >= 2):
+        return False
+    if c_attn.out_features != 3 * n_embd or n_embd % n_head:
+        return False
+    sq = mask.reshape(-1, *mask.shape[-2:])[0]
+    return sq.shape[0] == sq.shape[1] and bool(torch.equal(sq != 0, torch.ones_like(sq, dtype=torch.bool).tril()))
 
 
 def _is_encoder_attention(m: nn.Module) -> bool:
@@ -339,6 +382,10 @@ class OptimizedModelContext:
                 self._count("attention")
             elif _is_encoder_attention(m) and "flash_attention" in k:
                 self._set(name, EncoderAttentionWrapper(m, "matmul" in k))
+                taken.update(n for n, _ in m.named_modules(prefix=name))
+                self._count("attention")
+            elif _is_fused_qkv_causal_attention(m) and "flash_attention" in k:
+                self._set(name, FusedQKVAttentionWrapper(m, "matmul" in k))
                 taken.update(n for n, _ in m.named_modules(prefix=name))
                 self._count("attention")
             elif "fused_mlp" in k and _swiglu_parts(m) is not None and not isinstance(m, nn.Linear):

@@ -155,3 +155,51 @@ def test_bert_shaped_encoder_all_ops(gpu):
     assert torch.equal(via_wrapper, direct)
     c = verify.compare_outputs(ref, out, torch.float16, 1e-2, 1e-2)
     assert c["correctness"] == "PASS", c
+
+
+class _Gpt2CausalAttention(torch.nn.Module):
+    """GPT-2's attention module layout (models/gpt2.py:18-54): fused c_attn, tril mask buffer."""
+
+    def __init__(self, dim, heads, block):
+        super().__init__()
+        self.n_head, self.n_embd = heads, dim
+        self.c_attn, self.c_proj = torch.nn.Linear(dim, 3 * dim), torch.nn.Linear(dim, dim)
+        self.attn_dropout, self.resid_dropout = torch.nn.Dropout(0.0), torch.nn.Dropout(0.0)
+        self.register_buffer("bias", torch.ones(block, block).tril().view(1, 1, block, block))
+
+    def forward(self, x):
+        B, T, C = x.shape
+        q, k, v = (t.view(B, T, self.n_head, C // self.n_head).transpose(1, 2) for t in self.c_attn(x).split(C, 2))
+        att = (q.float() @ k.float().transpose(-2, -1)) * (C // self.n_head) ** -0.5  # fp32 reference
+        att = att.masked_fill(self.bias[:, :, :T, :T] == 0, float("-inf"))
+        y = (torch.softmax(att, dim=-1) @ v.float()).to(x.dtype)
+        return self.resid_dropout(self.c_proj(y.transpose(1, 2).reshape(B, T, C)))
+
+
+class _Gpt2RefBlock(torch.nn.Module):
+    def __init__(self, dim, heads, block):
+        super().__init__()
+        self.ln_1, self.ln_2 = torch.nn.LayerNorm(dim), torch.nn.LayerNorm(dim)
+        self.attn = _Gpt2CausalAttention(dim, heads, block)
+        self.mlp = torch.nn.Sequential(torch.nn.Linear(dim, 4 * dim), torch.nn.GELU(), torch.nn.Linear(4 * dim, dim))
+
+    def forward(self, x):
+        x = x + self.attn(self.ln_1(x))
+        return x + self.mlp(self.ln_2(x))
+
+
+def test_gpt2_reference_layout_attention(gpu):
+    """Blocks with GPT-2's attention layout: the fused-QKV causal strategy reads q, k, v as column
+    slices of the c_attn output; the whole model stays within the f16 tolerance of the reference."""
+    torch.manual_seed(0)
+    with torch.device(gpu):
+        m = torch.nn.Sequential(*[_Gpt2RefBlock(256, 4, 256) for _ in range(2)]).half().eval()
+        x = torch.randn(2, 200, 256).half()
+    with torch.no_grad():
+        ref = m(x)
+        ctx = verify.OptimizedModelContext(m, verify.ALL_KERNELS)
+        with ctx as pm:
+            out = pm(x)
+    assert ctx.applied == {"attention": 2, "matmul": 4, "layernorm": 4}, ctx.applied  # c_attn / c_proj run inside the wrapper
+    c = verify.compare_outputs(ref, out, torch.float16, 1e-2, 1e-2)
+    assert c["correctness"] == "PASS", c

@@ -100,3 +100,37 @@ def test_encoder_attention_strategy_applies_and_restores():
         assert isinstance(m[0].attention, verify.EncoderAttentionWrapper)
         assert isinstance(m[1].mlp[0], verify.LinearWrapper)
     assert {n: type(x) for n, x in m.named_modules()} == before
+
+
+class _Gpt2Attention(nn.Module):
+    """GPT-2-shaped causal attention: fused c_attn, explicit tril mask buffer, materialised scores."""
+
+    def __init__(self, dim, heads, block, causal=True):
+        super().__init__()
+        self.n_head, self.n_embd = heads, dim
+        self.c_attn, self.c_proj = nn.Linear(dim, 3 * dim), nn.Linear(dim, dim)
+        self.attn_dropout, self.resid_dropout = nn.Dropout(0.0), nn.Dropout(0.0)
+        import torch
+        m = torch.ones(block, block)
+        self.register_buffer("bias", (m.tril() if causal else m).view(1, 1, block, block))
+
+    def forward(self, x):
+        import math
+        import torch
+        B, T, C = x.shape
+        q, k, v = (t.view(B, T, self.n_head, C // self.n_head).transpose(1, 2) for t in self.c_attn(x).split(C, 2))
+        att = (q @ k.transpose(-2, -1).contiguous()) * (1.0 / math.sqrt(C // self.n_head))
+        att = att.masked_fill(self.bias[:, :, :T, :T] == 0, float("-inf"))
+        att = self.attn_dropout(torch.softmax(att.float(), dim=-1).to(x.dtype))
+        return self.resid_dropout(self.c_proj((att @ v).transpose(1, 2).reshape(B, T, C)))
+
+
+def test_fused_qkv_causal_attention_strategy():
+    m = nn.ModuleList([_Gpt2Attention(64, 4, 32), _Gpt2Attention(64, 4, 32, causal=False)])
+    before = {n: type(x) for n, x in m.named_modules()}
+    ctx = verify.OptimizedModelContext(m, verify.ALL_KERNELS)
+    with ctx:
+        assert isinstance(m[0], verify.FusedQKVAttentionWrapper)
+        assert not isinstance(m[1], verify.FusedQKVAttentionWrapper), "a non-causal mask must not be swapped"
+        assert ctx.applied == {"attention": 1, "matmul": 2}, ctx.applied
+    assert {n: type(x) for n, x in m.named_modules()} == before
