@@ -66,6 +66,26 @@ def reduce_max(x, dim=-1):
     return x.max(dim=dim).values
 
 
+def _mm_checked(a, b):
+    """a @ b; for fp32 the correctly rounded product (fp64 accumulation, one rounding to fp32)."""
+    if a.dtype == torch.float32:
+        return torch.matmul(a.double(), b.double()).float()
+    return torch.matmul(a, b)
+
+
+def fused_mlp_checked(x, w_gate, w_up, w_down, activation="silu"):
+    """fused_mlp with every matrix product correctly rounded for fp32 (as _mm_checked)."""
+    g = _mm_checked(x, w_gate.T)
+    u = _mm_checked(x, w_up.T)
+    if activation == "silu":
+        g = F.silu(g)
+    elif activation == "gelu":
+        g = F.gelu(g)
+    elif activation == "relu2":
+        g = F.relu(g) ** 2
+    return _mm_checked(g * u, w_down.T)
+
+
 # keyword-dict wrappers keyed like the op table
 BASELINE = {
     "matmul": lambda i: matmul(i["A"], i["B"]),
@@ -78,3 +98,11 @@ BASELINE = {
     "rotary_embedding": lambda i: rotary_embedding(i["x"], i["cos"], i["sin"]),
     "reduce": lambda i: reduce_sum(i["x"]),
 }
+
+# Correctness references of the harness: BASELINE, except that fp32 matrix products are checked
+# against the correctly rounded product. Two fp32 summation orders over K = 8192 of N(0, 1) terms
+# differ by ~1e-3, above the op table's fp32 tolerance (1e-4), so stock fp32 torch.matmul cannot
+# referee a fp32 GEMM at that tolerance; it stays the timing baseline.
+CHECK = dict(BASELINE)
+CHECK["matmul"] = lambda i: _mm_checked(i["A"], i["B"])
+CHECK["fused_mlp"] = lambda i: fused_mlp_checked(i["x"], i["w_gate"], i["w_up"], i["w_down"])

@@ -917,6 +917,19 @@ static void launch_dma_kernel(const void* A, const void* B0, const void* B1, voi
 #ifndef AK_GEMM_PLAN
 #define AK_GEMM_PLAN 2
 #endif
+// Waves along N of the 128x128 tile: 4 (8 waves of 64x32, two per SIMD) or 2 (4 waves of 64x64,
+// one per SIMD). Measured, cold, 2048^3 (256 tiles, one per CU): f16 NN 26.8 us with 8 waves against
+// 36.5 us with 4 (stock hipBLASLt 32.0), bf16 NT 26.4 against 36.0 (28.9); three or four stages for
+// the 4-wave tile reach 28.2-29.4 us. Shapes on other tiles are unchanged.
+#ifndef AK_GEMM_SMALL_WN
+#define AK_GEMM_SMALL_WN 4
+#endif
+constexpr int kSmallWN = AK_GEMM_SMALL_WN;
+// stages for 4-wave tiles under plan 2: 2, or up to this many where they fit
+#ifndef AK_GEMM_NS4
+#define AK_GEMM_NS4 2
+#endif
+
 template <int BM, int BN, int NB, int NW>
 struct DmaPlan {
   static constexpr int kStage64 = (BM + NB * BN) * 64 * 2;
@@ -928,7 +941,8 @@ struct DmaPlan {
   // 107.4 us two-stage (plan 3: 121.2 us, the doubled barrier count outweighs the deeper queue).
   static constexpr int BKD = (AK_GEMM_PLAN == 3 && kOk32) ? 32 : 64;
   static constexpr int NS = AK_GEMM_PLAN == 1 ? 2
-                            : AK_GEMM_PLAN == 2 ? (kFit64 >= 3 && NW == 8 ? 3 : 2)
+                            : AK_GEMM_PLAN == 2 ? (kFit64 >= 3 && NW == 8 ? 3
+                                                   : (NW == 4 ? (kFit64 < AK_GEMM_NS4 ? kFit64 : AK_GEMM_NS4) : 2))
                             : (kOk32 ? 4 : 2);
 };
 
@@ -967,7 +981,7 @@ static void launch_gemm_dma(const void* A, const void* B0, const void* B1, void*
     if (t.bm == 256 && t.bn == 256)
       launch_dma_cfg<T, 256, 256, 2, kBigWN, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
     else if (t.bm == 256) launch_dma_cfg<T, 256, 128, 4, 2, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
-    else launch_dma_cfg<T, 128, 128, 2, 2, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
+    else launch_dma_cfg<T, 128, 128, 2, kSmallWN, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
   } else {
     static_assert(!BKN, "gate/up weights are [H, D]");
     if (t.bm == 256 && t.bn == 256)
