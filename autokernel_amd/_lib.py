@@ -41,6 +41,8 @@ SIGNATURES: dict[str, list] = {
     "ak_reduce_max": [_i, _p, _p, _i64, _i64, _i64, _p],
     "ak_gemm": [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],
     "ak_gemm_residual": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],
+    "ak_gemm_workspace_bytes": [_i, _i64, _i64, _i64, _i64, _i64, _i64, _i],
+    "ak_gemm_ws": [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p, _i64, _p],
     "ak_gemm_rope": [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p, _p, _i64, _i64, _i64, _p],
     "ak_mlp_gate_up": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i, _p],
     "ak_transpose": [_i, _p, _p, _i64, _i64, _i64, _i64, _p],
@@ -50,6 +52,7 @@ SIGNATURES: dict[str, list] = {
                           _pi64, _pi64, _pi64, _pi64, _i, _f, _p],
 }
 _STR_FUNCS = ("ak_version", "ak_status_string", "ak_last_hip_error_string")
+_I64_FUNCS = ("ak_gemm_workspace_bytes",)  # return int64_t instead of a status
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -74,7 +77,7 @@ def load() -> ctypes.CDLL:
             for name, args in SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.argtypes = args
-                fn.restype = ctypes.c_int
+                fn.restype = ctypes.c_int64 if name in _I64_FUNCS else ctypes.c_int
             for name in _STR_FUNCS:
                 fn = getattr(lib, name)
                 fn.restype = ctypes.c_char_p

@@ -113,17 +113,24 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int* tm, i
 // --------------------------------------------------------------------------------------------
 // Epilogues (applied to fp32 accumulators; every step rounds like the reference's tensor ops)
 // --------------------------------------------------------------------------------------------
-enum Epi { kEpiStore = 0, kEpiSilu = 1, kEpiGelu = 2, kEpiRelu2 = 3, kEpiNone = 4, kEpiResidual = 5, kEpiRope = 6 };
+enum Epi { kEpiStore = 0, kEpiSilu = 1, kEpiGelu = 2, kEpiRelu2 = 3, kEpiNone = 4, kEpiResidual = 5, kEpiRope = 6,
+           kEpiPartial = 7 };
 
 // Arguments of the rotary epilogue (kEpiRope), passed by value to every f16 / bf16 GEMM kernel:
 // columns [0, rot_cols) of C form heads of head_dim columns whose (even, odd) pairs are rotated
 // by the fp32 tables cos / sin [seq_len, head_dim / 2]; row m of C is token m % seq_len.
+//
+// Split-K (kEpiPartial): the grid's y dimension is the K slice; slice z multiplies A and B advanced
+// by z * split_a / z * split_b elements and stores its fp32 accumulators to the workspace advanced by
+// z * split_c floats (row stride ldc), for splitk_reduce to sum.
 struct EpiArgs {
   const float* cos = nullptr;
   const float* sin = nullptr;
   int head_dim = 0;
   int rot_cols = 0;
   int seq_len = 1;
+  int splits = 1;
+  int64_t split_a = 0, split_b = 0, split_c = 0;
 };
 
 // The model's rotation of one pair in fp32, each product and sum rounded on its own (no fused
@@ -169,6 +176,21 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   constexpr bool kRes = NB == 1 && EPI == kEpiResidual;
   constexpr bool kRope = NB == 1 && EPI == kEpiRope;
+  if constexpr (NB == 1 && EPI == kEpiPartial) {
+    // fp32 accumulators as they are (C is the fp32 workspace; N % 4 == 0 and ldc % 4 == 0)
+    float* Cf = reinterpret_cast<float*>(C);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int m = mb + i * MST;
+      if (m >= M) continue;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = nb + j * NST;
+        if (n < N) *reinterpret_cast<f32x4*>(Cf + (int64_t)m * ldc + n) = acc[0][i][j];
+      }
+    }
+    return;
+  }
   u32x2 side_r[kRes ? FM : 1][kRes ? FN : 1];
   f32x2 side_c[kRope ? FM : 1][kRope ? FN : 1], side_s[kRope ? FM : 1][kRope ? FN : 1];
   if constexpr (kRes) {
@@ -614,6 +636,12 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
   __shared__ __attribute__((aligned(1024))) uint16_t sS2[NS > 2 ? kStage : 1];
   __shared__ __attribute__((aligned(1024))) uint16_t sS3[NS > 3 ? kStage : 1];
 
+  if constexpr (EPI == kEpiPartial) {
+    const int z = (int)blockIdx.y;  // K slice
+    A += z * ep.split_a;
+    B0 += z * ep.split_b;
+    C += 2 * z * ep.split_c;  // fp32 workspace addressed in 16-bit units
+  }
   int tm, tn;
   tile_coords(tiles_m, tiles_n, &tm, &tn);
   const int m0 = tm * BM, n0 = tn * BN;
@@ -907,7 +935,7 @@ static void launch_dma_kernel(const void* A, const void* B0, const void* B1, voi
   // and B is nn.Linear-layout; else 16x16x32
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int MF = (kGemmMF == 32 && !BKN && WTN % 32 == 0 && (WTM / 32) % 2 == 0) ? 32 : 16;
-  gemm_dma<T, BM, BN, WM, WN, NB, EPI, BKD, NS, BKN, MF><<<tiles_m * tiles_n, WM * WN * kWave, 0, s>>>(
+  gemm_dma<T, BM, BN, WM, WN, NB, EPI, BKD, NS, BKN, MF><<<dim3(tiles_m * tiles_n, ep.splits), WM * WN * kWave, 0, s>>>(
       (const uint16_t*)A, (const uint16_t*)B0, (const uint16_t*)B1, (uint16_t*)C, M, N, K, lda, ldb, ldc,
       tiles_m, tiles_n, ep);
 }
@@ -956,7 +984,7 @@ static void launch_dma_cfg(const void* A, const void* B0, const void* B1, void* 
   // 64-deep pair is faster per tile (2048x6144x4096 on 192 tiles of 256x256: 109.9 us against
   // 127.5 us).
   constexpr bool kOk32 = P::kOk32;
-  if (kOk32 && kUseDeep && 2 * tiles_m * tiles_n <= kCUs) {
+  if (kOk32 && kUseDeep && 2 * tiles_m * tiles_n * ep.splits <= kCUs) {
     if constexpr (kOk32)
       launch_dma_kernel<T, BM, BN, WM, WN, NB, EPI, 32, 4, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, tiles_m,
                                                                 tiles_n, s, ep);
@@ -1024,6 +1052,66 @@ static int launch_gemm16(const void* A, const void* B0, const void* B1, void* C,
       return AK_EINVAL;
     }
   }
+  return record_launch();
+}
+
+// ---------------------------------------------------------------------------------------------
+// Split-K for grids that leave most CUs idle (few output tiles, long K): slice z of the K range runs
+// as grid row z of the LDS-DMA kernel and stores fp32 partial tiles to the caller's workspace
+// [splits][M][N]; splitk_reduce then adds the slices in order z = 0, 1, ... and rounds once, so the
+// result is deterministic and keeps "fp32 accumulation, one output rounding".
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ ws, uint16_t* __restrict__ C, int M,
+                                                     int N, int64_t ldc, int splits) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // one 4-column group per thread
+  const int groups_per_row = N / 4;
+  if (i >= (int64_t)M * groups_per_row) return;
+  const int m = (int)(i / groups_per_row), n = (int)(i % groups_per_row) * 4;
+  const int64_t plane = (int64_t)M * N;
+  const float* p = ws + (int64_t)m * N + n;
+  f32x4 acc = *reinterpret_cast<const f32x4*>(p);
+  for (int z = 1; z < splits; ++z) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p + z * plane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += v[e];
+  }
+  u32x2 o;
+  o[0] = (uint32_t)T::from_f(acc[0]) | ((uint32_t)T::from_f(acc[1]) << 16);
+  o[1] = (uint32_t)T::from_f(acc[2]) | ((uint32_t)T::from_f(acc[3]) << 16);
+  *reinterpret_cast<u32x2*>(C + (int64_t)m * ldc + n) = o;
+}
+
+// K slices for a plain f16 / bf16 GEMM on the LDS-DMA path, 1 when splitting does not pay: the
+// chosen tiling must fill at most half the CUs, each slice keeps at least 256 of K (four 64-deep
+// tiles) and a multiple of 64, and slices stop doubling once tiles x slices would pass the CU count.
+static int splitk_slices(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, bool bt) {
+  if (M <= 0 || N <= 0 || K <= 0 || N % 4 != 0 || ldc % 4 != 0 || lda % 8 != 0 || ldb % 8 != 0) return 1;
+  if (M * lda >= INT_MAX || (bt ? N : K) * ldb >= INT_MAX || M * N * 8 >= INT_MAX) return 1;
+  if (!bt && N < 8) return 1;
+  const TileCfg t = pick_tile(M, N, 1, !bt);
+  const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
+  if (2 * tiles > kCUs) return 1;
+  int s = 1;
+  while (s < 8 && tiles * s * 2 <= kCUs && K % (64 * s * 2) == 0 && K / (s * 2) >= 256) s *= 2;
+  return s;
+}
+
+template <typename T>
+static int launch_gemm16_splitk(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                                int64_t lda, int64_t ldb, int64_t ldc, bool bt, int splits, float* ws,
+                                hipStream_t s) {
+  EpiArgs ep;
+  ep.splits = splits;
+  const int64_t ks = K / splits;
+  ep.split_a = ks;
+  ep.split_b = bt ? ks : ks * ldb;
+  ep.split_c = M * N;
+  // partial tiles: the workspace is the output, row stride N
+  if (bt) launch_gemm_dma<T, 1, kEpiPartial, false>(A, B, nullptr, ws, (int)M, (int)N, (int)ks, lda, ldb, N, s, ep);
+  else launch_gemm_dma<T, 1, kEpiPartial, true>(A, B, nullptr, ws, (int)M, (int)N, (int)ks, lda, ldb, N, s, ep);
+  const int64_t groups = M * (N / 4);
+  splitk_reduce<T><<<(unsigned)cdiv(groups, 256), 256, 0, s>>>(ws, (uint16_t*)C, (int)M, (int)N, ldc, splits);
   return record_launch();
 }
 
@@ -1146,6 +1234,29 @@ extern "C" int ak_gemm(int dtype, const void* A, const void* B, void* C, int64_t
     case AK_BF16: return launch_gemm16<TBF16, 1, kEpiStore>(A, B, nullptr, C, M, N, K, lda, ldb, ldc, bt, stream);
     default: return AK_EINVAL;
   }
+}
+
+extern "C" int64_t ak_gemm_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                                           int64_t ldc, int b_trans) {
+  if (dtype != AK_F16 && dtype != AK_BF16) return 0;
+  if (M < 0 || N < 0 || K < 0 || M > INT_MAX || N > INT_MAX || K > INT_MAX) return 0;
+  const int sl = splitk_slices(M, N, K, lda, ldb, ldc, b_trans != 0);
+  return sl > 1 ? (int64_t)sl * M * N * (int64_t)sizeof(float) : 0;
+}
+
+extern "C" int ak_gemm_ws(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                          int64_t lda, int64_t ldb, int64_t ldc, int b_trans, void* workspace,
+                          int64_t workspace_bytes, hipStream_t stream) {
+  const int64_t need = ak_gemm_workspace_bytes(dtype, M, N, K, lda, ldb, ldc, b_trans);
+  const bool aligned = host_aligned16(A) && host_aligned16(B) && (((uintptr_t)C) & 7u) == 0 &&
+                       host_aligned16(workspace);
+  if (need == 0 || !workspace || workspace_bytes < need || !aligned || lda < K || ldc < N ||
+      ldb < (b_trans ? K : N))
+    return ak_gemm(dtype, A, B, C, M, N, K, lda, ldb, ldc, b_trans, stream);
+  const int sl = (int)(need / (M * N * (int64_t)sizeof(float)));
+  if (dtype == AK_F16)
+    return launch_gemm16_splitk<TF16>(A, B, C, M, N, K, lda, ldb, ldc, b_trans != 0, sl, (float*)workspace, stream);
+  return launch_gemm16_splitk<TBF16>(A, B, C, M, N, K, lda, ldb, ldc, b_trans != 0, sl, (float*)workspace, stream);
 }
 
 extern "C" int ak_gemm_residual(int dtype, const void* A, const void* B, const void* R, void* C, int64_t M,

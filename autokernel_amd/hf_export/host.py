@@ -166,8 +166,9 @@ def reduce_max(x: torch.Tensor, dim: int = -1) -> torch.Tensor:
     return _reduce(x, dim, True)
 
 
-def _gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """C = A @ B for 2-D A [M, K] and B [K, N]; a transposed [N, K] view of B is read in place."""
+def _gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, split_k: bool = False) -> torch.Tensor:
+    """C = A @ B for 2-D A [M, K] and B [K, N]; a transposed [N, K] view of B is read in place.
+    split_k: grids that leave most CUs idle split K (the matmul op does; fused_mlp does not)."""
     M, K = A.shape
     K2, N = B.shape
     if K != K2:
@@ -185,14 +186,22 @@ def _gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> 
     C = out if out is not None else torch.empty((M, N), device=A.device, dtype=A.dtype)
     if K == 0:
         return C.zero_()
-    ops.gemm(C, A, Bs, bt)
+    ws = None
+    if split_k:
+        def ld(t):
+            return t.stride(0) if t.shape[0] > 1 else max(t.shape[1], 1)
+        code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[A.dtype]
+        nbytes = ops.gemm_workspace_bytes(code, M, N, K, ld(A), ld(Bs), ld(C), bt)
+        if nbytes > 0:
+            ws = torch.empty(nbytes // 4, device=A.device, dtype=torch.float32)
+    ops.gemm(C, A, Bs, bt, ws)
     return C
 
 
 def matmul(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     _check("matmul", A, B)
     if A.dim() == 1 and B.dim() == 1:
-        return _gemm(A.view(1, -1), B.view(-1, 1)).view(())
+        return _gemm(A.view(1, -1), B.view(-1, 1), split_k=True).view(())
     if A.dim() == 1:
         return matmul(A.view(1, -1), B).squeeze(-2)
     if B.dim() == 1:
@@ -200,13 +209,13 @@ def matmul(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     if B.dim() == 2:
         lead = A.shape[:-1]
         A2 = A.reshape(-1, A.shape[-1]) if A.dim() > 2 else A
-        return _gemm(A2, B).view(*lead, B.shape[-1])
+        return _gemm(A2, B, split_k=True).view(*lead, B.shape[-1])
     batch = torch.broadcast_shapes(A.shape[:-2], B.shape[:-2])
     Ab = A.expand(*batch, *A.shape[-2:]).reshape(-1, *A.shape[-2:])
     Bb = B.expand(*batch, *B.shape[-2:]).reshape(-1, *B.shape[-2:])
     C = torch.empty((Ab.shape[0], A.shape[-2], B.shape[-1]), device=A.device, dtype=A.dtype)
     for i in range(Ab.shape[0]):
-        _gemm(Ab[i], Bb[i], out=C[i])
+        _gemm(Ab[i], Bb[i], out=C[i], split_k=True)
     return C.view(*batch, A.shape[-2], B.shape[-1])
 
 

@@ -189,7 +189,8 @@ void ak_op_reduce_max(at::Tensor& y, const at::Tensor& x, int64_t outer, int64_t
 
 // c [M, N] = a [M, K] @ op(b): b is stored [K, N] (b_trans false) or [N, K] (b_trans true, an
 // nn.Linear weight). Every operand needs a unit stride along its last dim; row strides are passed.
-void ak_op_gemm(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, bool b_trans) {
+void ak_op_gemm(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, bool b_trans,
+                const std::optional<at::Tensor>& workspace) {
   const char* op = "matmul";
   on_gpu(a, a, op, "a");
   on_gpu(b, a, op, "b");
@@ -205,9 +206,25 @@ void ak_op_gemm(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, bool b_
     TORCH_CHECK(t->size(1) <= 1 || t->stride(1) == 1, op, ": operands need a unit stride along their last dim");
   auto ld = [](const at::Tensor& t) { return t.size(0) > 1 ? t.stride(0) : std::max<int64_t>(t.size(1), 1); };
   const c10::DeviceGuard g(a.device());
-  check_status(ak_gemm(dtype_code(a, op), a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, ld(a), ld(b),
-                       ld(c), b_trans ? 1 : 0, stream_of(a)),
+  const int code = dtype_code(a, op);
+  // a workspace (fp32, sized by gemm_workspace_bytes) lets under-filled grids split K
+  if (workspace.has_value() && workspace->numel() > 0) {
+    on_gpu(*workspace, a, op, "workspace", false);
+    dense(*workspace, op, "workspace");
+    TORCH_CHECK(workspace->scalar_type() == at::kFloat, op, ": workspace must be float32");
+    check_status(ak_gemm_ws(code, a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, ld(a), ld(b), ld(c),
+                            b_trans ? 1 : 0, workspace->data_ptr(), workspace->numel() * 4, stream_of(a)),
+                 "ak_gemm_ws");
+    return;
+  }
+  check_status(ak_gemm(code, a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, ld(a), ld(b), ld(c),
+                       b_trans ? 1 : 0, stream_of(a)),
                "ak_gemm");
+}
+
+int64_t ak_op_gemm_workspace_bytes(int64_t dtype, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                                   int64_t ldc, bool b_trans) {
+  return ak_gemm_workspace_bytes((int)dtype, M, N, K, lda, ldb, ldc, b_trans ? 1 : 0);
 }
 
 void ak_op_mlp_gate_up(at::Tensor& h, const at::Tensor& x, const at::Tensor& w_gate,
@@ -271,8 +288,10 @@ TORCH_LIBRARY_EXPAND(TORCH_EXTENSION_NAME, ops) {
   ops.impl("reduce_sum", c10::kCUDA, &ak_op_reduce_sum);
   ops.def("reduce_max(Tensor! y, Tensor x, int outer, int reduce, int inner) -> ()");
   ops.impl("reduce_max", c10::kCUDA, &ak_op_reduce_max);
-  ops.def("gemm(Tensor! c, Tensor a, Tensor b, bool b_trans) -> ()");
+  ops.def("gemm(Tensor! c, Tensor a, Tensor b, bool b_trans, Tensor(w!)? workspace) -> ()");
   ops.impl("gemm", c10::kCUDA, &ak_op_gemm);
+  ops.def("gemm_workspace_bytes(int dtype, int M, int N, int K, int lda, int ldb, int ldc, bool b_trans) -> int");
+  ops.impl("gemm_workspace_bytes", &ak_op_gemm_workspace_bytes);
   ops.def("mlp_gate_up(Tensor! h, Tensor x, Tensor w_gate, Tensor w_up, int activation) -> ()");
   ops.impl("mlp_gate_up", c10::kCUDA, &ak_op_mlp_gate_up);
   ops.def("flash_attn_fwd(Tensor! o, Tensor q, Tensor k, Tensor v, bool causal, float sm_scale) -> ()");

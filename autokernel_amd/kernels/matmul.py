@@ -4,7 +4,9 @@ Mirrors reference.py:10-12 and kernels/matmul.py:62. A: [..., M, K] (leading dim
 M when B is 2-D), B: [K, N]; batched B loops over the batch. When B is a transposed view of a
 row-major [N, K] tensor (nn.Linear's weight.t()), the GEMM reads it in place (b_trans = 1)
 instead of copying; a row-major [K, N] B is read in place too (b_trans = 0). Runs ak_gemm
-(gemm.hip).
+(gemm.hip), or, for kernel_fn, ak_gemm_ws with a torch-allocated fp32 workspace when few output tiles
+and a long K would leave most CUs idle (K split into slices that run side by side, then added in a
+fixed order).
 """
 from __future__ import annotations
 
@@ -39,8 +41,12 @@ def transpose(B: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """C = A @ B for 2-D A [M, K] and 2-D B [K, N] (B may be a transposed [N, K] view)."""
+def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, split_k: bool = False) -> torch.Tensor:
+    """C = A @ B for 2-D A [M, K] and 2-D B [K, N] (B may be a transposed [N, K] view).
+
+    split_k: let grids that leave most CUs idle split K (ak_gemm_ws); kernel_fn sets it. The model
+    plug-in's projections keep the unsplit kernel, whose fp32 summation order reproduces stock
+    PyTorch's f16 logits bit for bit."""
     M, K = A.shape
     K2, N = B.shape
     if K != K2:
@@ -55,10 +61,18 @@ def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None) -> t
     C = out if out is not None else torch.empty((M, N), device=A.device, dtype=A.dtype)
     if K == 0:
         return C.zero_()
+    lib = _lib.load()
+    ldc = C.stride(0) if M > 1 else max(N, 1)
     with device_guard(A):
-        st = _lib.load().ak_gemm(code, A.data_ptr(), Bt.data_ptr(), C.data_ptr(), M, N, K,
-                                 lda, ldb, C.stride(0) if M > 1 else max(N, 1), bt,
-                                 _lib.stream_of(A))
+        # grids that leave most CUs idle split K over a torch-allocated fp32 workspace (ak_gemm_ws)
+        ws_bytes = lib.ak_gemm_workspace_bytes(code, M, N, K, lda, ldb, ldc, bt) if split_k else 0
+        if ws_bytes > 0:
+            ws = torch.empty(ws_bytes // 4, device=A.device, dtype=torch.float32)
+            st = lib.ak_gemm_ws(code, A.data_ptr(), Bt.data_ptr(), C.data_ptr(), M, N, K, lda, ldb, ldc, bt,
+                                ws.data_ptr(), ws_bytes, _lib.stream_of(A))
+        else:
+            st = lib.ak_gemm(code, A.data_ptr(), Bt.data_ptr(), C.data_ptr(), M, N, K, lda, ldb, ldc, bt,
+                             _lib.stream_of(A))
     _lib.check(st, "ak_gemm", M=M, N=N, K=K, b_trans=bt, dtype=A.dtype)
     return C
 
@@ -122,7 +136,7 @@ def gemm_rope(A: torch.Tensor, B: torch.Tensor, cos: torch.Tensor, sin: torch.Te
 def kernel_fn(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     _lib.require_gpu("matmul", A, B)
     if A.dim() == 1 and B.dim() == 1:
-        return gemm(A.view(1, -1), B.view(-1, 1)).view(())
+        return gemm(A.view(1, -1), B.view(-1, 1), split_k=True).view(())
     if A.dim() == 1:
         return kernel_fn(A.view(1, -1), B).squeeze(-2)
     if B.dim() == 1:
@@ -130,12 +144,12 @@ def kernel_fn(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     if B.dim() == 2:
         lead = A.shape[:-1]
         A2 = A.reshape(-1, A.shape[-1]) if A.dim() > 2 else A
-        return gemm(A2, B).view(*lead, B.shape[-1])
+        return gemm(A2, B, split_k=True).view(*lead, B.shape[-1])
     # batched B: broadcast batch dims, one GEMM per batch entry
     batch = torch.broadcast_shapes(A.shape[:-2], B.shape[:-2])
     Ab = A.expand(*batch, *A.shape[-2:]).reshape(-1, *A.shape[-2:])
     Bb = B.expand(*batch, *B.shape[-2:]).reshape(-1, *B.shape[-2:])
     C = torch.empty((Ab.shape[0], A.shape[-2], B.shape[-1]), device=A.device, dtype=A.dtype)
     for i in range(Ab.shape[0]):
-        gemm(Ab[i], Bb[i], out=C[i])
+        gemm(Ab[i], Bb[i], out=C[i], split_k=True)
     return C.view(*batch, A.shape[-2], B.shape[-1])

@@ -153,6 +153,24 @@ int ak_gemm(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t
             int64_t lda, int64_t ldb, int64_t ldc, int b_trans, hipStream_t stream);
 
 /*
+ * Split-K GEMM for grids that leave most compute units idle (few output tiles, long K), e.g.
+ * 1024 x 1024 x 8192. Same arguments and result semantics as ak_gemm (fp32 accumulation, one output
+ * rounding; deterministic), plus a caller-owned fp32 workspace.
+ *   ak_gemm_workspace_bytes: bytes of workspace ak_gemm_ws uses for this problem; 0 when it would
+ *     not split (fp32, grids that fill the GPU, K too short), and then needs none.
+ *   ak_gemm_ws: splits K into slices that run side by side, each storing fp32 partial tiles to the
+ *     workspace ([slices][M][N]), then adds the slices in a fixed order and rounds once. With too
+ *     small a workspace (or NULL), or unaligned operands, it runs ak_gemm instead.
+ * Replaces: reference.py:10-12 matmul_ref for the reference harness's under-filled shapes
+ *           (bench.py:336-345: tiny .. medium, deep_k); no counterpart in the starters.
+ */
+int64_t ak_gemm_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                                int64_t ldc, int b_trans);
+int ak_gemm_ws(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+               int64_t lda, int64_t ldb, int64_t ldc, int b_trans, void* workspace, int64_t workspace_bytes,
+               hipStream_t stream);
+
+/*
  * GEMM with the residual add of a transformer block in its epilogue: C = R + A * op(B), with
  * A, B, b_trans, lda, ldb as in ak_gemm. The product is rounded to the element type, R is added
  * and the sum rounded again, so C equals ak_gemm followed by a separate element-type add, bit for

@@ -544,3 +544,25 @@ def test_attention_random_shapes(gpu, B, Hq, Hk, Sq, Sk, D, dt, causal):
     tol = 1e-4 if dt == torch.float32 else 1e-2
     # top-left causal mask: query i always sees key 0, so no row is empty
     assert_close(out, exp, tol, tol, f"attention {B}x{Hq}/{Hk}x{Sq}x{Sk}x{D} {dt} causal={causal}")
+
+
+@pytest.mark.parametrize("M,N,K,bt", [(1024, 1024, 8192, True), (1024, 1024, 8192, False), (1024, 1024, 1024, False),
+                                      (128, 128, 4096, True), (300, 520, 2048, True), (512, 200, 4096, False)])
+def test_gemm_split_k(gpu, M, N, K, bt):
+    """Under-filled grids with a long K run split-K (ak_gemm_ws, matmul's kernel_fn path): within the
+    harness tolerance of the oracle in f16 / bf16, both B layouts, ragged tiles, and bitwise
+    reproducible run to run."""
+    from autokernel_amd import _lib
+    from autokernel_amd.kernels.matmul import gemm
+    lib = _lib.load()
+    for dt in (torch.float16, torch.bfloat16):
+        g = torch.Generator().manual_seed(M + N + K + int(bt))
+        A = (torch.randn(M, K, generator=g) / K ** 0.5).to(dt)
+        W = torch.randn(N, K, generator=g).to(dt)
+        Bd = W.to(gpu).t() if bt else W.t().contiguous().to(gpu)
+        code = _lib.dtype_code(A, "mm")
+        ldb = K if bt else N
+        assert lib.ak_gemm_workspace_bytes(code, M, N, K, K, ldb, N, int(bt)) > 0, "expected a split"
+        outs = [gemm(A.to(gpu), Bd, split_k=True) for _ in range(3)]
+        assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+        assert_close(outs[0], R.matmul_ref(A.float(), W.float().T).to(dt), 2e-2, 2e-2, f"split {M}x{N}x{K} {dt}")
