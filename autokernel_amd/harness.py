@@ -457,6 +457,11 @@ def kernel_configs() -> Dict[str, dict]:
         c = dict(cfg)
         c["reference_fn"] = baseline_torch.BASELINE[name]
         c["check_fn"] = baseline_torch.CHECK[name]
+        if name == "layernorm":
+            # The table's bf16 tolerance (2e-3) is below one bf16 rounding step (2^-8 relative): two
+            # fp32 LayerNorms round rare near-tie values to neighbouring bf16 values (measured: one
+            # step, up to 1.56e-2 at |y| in [2, 4)). bf16 is checked at the north star's 1e-2.
+            c["tolerances"] = {**cfg["tolerances"], torch.bfloat16: {"atol": 1e-2, "rtol": 1e-2}}
         out[name] = c
     return out
 
