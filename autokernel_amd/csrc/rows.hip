@@ -8,6 +8,7 @@
 namespace ak {
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kLoopThreads = 256;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -285,6 +286,78 @@ __device__ __forceinline__ void block_combine_ms(OnlineMS a, float* red, float* 
   *S = tot;
 }
 
+// Wide rows that do not vectorise (a width that is not a multiple of the 16-byte vector, e.g. a
+// 50257-entry vocabulary): one row per block of 1024 threads, element c = tid + 1024 k cached in
+// registers (EPT per thread, so x is read once), with the vector path's arithmetic.
+// Rows are addressed through a buffer resource spanning the row (gfx9 descriptor word 3 =
+// 0x00020000, raw 32-bit data format, stride 0, num_records = the row's bytes): element c is one
+// per-thread VGPR offset plus a uniform scalar offset, where 64-bit pointers would take two VGPRs
+// per element and spill at this many elements per thread.
+constexpr int kWideThreads = 1024;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* row, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(row), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ void buf_ld(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint16_t& v) {
+  v = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+__device__ __forceinline__ void buf_ld(__amdgpu_buffer_rsrc_t r, int voff, int soff, float& v) {
+  v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ void buf_st(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint16_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, r, voff, soff, 0);
+}
+__device__ __forceinline__ void buf_st(__amdgpu_buffer_rsrc_t r, int voff, int soff, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, soff, 0);
+}
+
+// Loads this thread's EPT elements of the row (c = tid + 1024 k, c < cols) into v and returns
+// their maximum (-inf for a thread with none). Every load is issued before the first use so all
+// of them are in flight together, with no branch: a thread past the row's end re-reads element
+// cols - 1 (so every access stays in the row; a wave's such loads share one cache line) and takes
+// -inf by a select.
+template <typename T, int EPT>
+__device__ __forceinline__ float wide_load_max(const typename T::S* xr, int cols, float (&v)[EPT]) {
+  using S = typename T::S;
+  const __amdgpu_buffer_rsrc_t r = row_rsrc(xr, cols * (int)sizeof(S));
+  S e[EPT];
+#pragma unroll
+  for (int k = 0; k < EPT; ++k)
+    buf_ld(r, min((int)threadIdx.x + k * kWideThreads, cols - 1) * (int)sizeof(S), 0, e[k]);
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    v[k] = (int)threadIdx.x + k * kWideThreads < cols ? T::to_f(e[k]) : -INFINITY;
+    m = fmaxf(m, v[k]);
+  }
+  return m;
+}
+
+template <typename T, int EPT>
+__global__ __launch_bounds__(kWideThreads) void softmax_wide(const typename T::S* __restrict__ x,
+                                                             typename T::S* __restrict__ y, int cols) {
+  __shared__ float red[kWideThreads / kWave];
+  const int64_t base = (int64_t)blockIdx.x * cols;
+  float v[EPT];
+  float m = group_reduce<kWideThreads, 1>(wide_load_max<T, EPT>(x + base, cols, v), red);
+  const float mb = m * kLog2e;
+  // p is recomputed in the write pass rather than kept (the same expression, so the same value):
+  // holding both x and p would spill at 64 elements per thread.
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < EPT; ++k)
+    if (threadIdx.x + k * kWideThreads < cols) s += fast_exp2(__builtin_fmaf(v[k], kLog2e, -mb));
+  s = group_reduce<kWideThreads, 0>(s, red);
+  const float inv = 1.0f / s;
+  using S = typename T::S;
+  const __amdgpu_buffer_rsrc_t r = row_rsrc(y + base, cols * (int)sizeof(S));
+  const int voff = threadIdx.x * (int)sizeof(S);
+#pragma unroll
+  for (int k = 0; k < EPT; ++k)
+    if (threadIdx.x + k * kWideThreads < cols)
+      buf_st(r, voff, k * kWideThreads * (int)sizeof(S), T::from_f(fast_exp2(__builtin_fmaf(v[k], kLog2e, -mb)) * inv));
+}
+
 template <typename T>
 __global__ __launch_bounds__(kLoopThreads) void softmax_loop(
     const typename T::S* __restrict__ x, typename T::S* __restrict__ y, int cols) {
@@ -295,10 +368,12 @@ __global__ __launch_bounds__(kLoopThreads) void softmax_loop(
   for (int c = threadIdx.x; c < cols; c += kLoopThreads) a.add(T::to_f(xr[c]));
   float M, S;
   block_combine_ms(a, red, &M, &S);
+  // The write pass uses the online pass's exponent form, (x - M) log2 e. The fused form
+  // x log2 e - round(M log2 e) of the cached kernels would shift every exponent by the rounding of
+  // M log2 e (0.008 at |M| ~ 1e5), a scale that S, summed in the other form, does not share.
   const float inv = 1.0f / S;
-  const float mb = M * kLog2e;
   for (int c = threadIdx.x; c < cols; c += kLoopThreads)
-    yr[c] = T::from_f(fast_exp2(__builtin_fmaf(T::to_f(xr[c]), kLog2e, -mb)) * inv);
+    yr[c] = T::from_f(fast_exp2((T::to_f(xr[c]) - M) * kLog2e) * inv);
 }
 
 template <typename T>
@@ -314,6 +389,13 @@ static int launch_softmax(const void* x, void* y, int64_t rows, int64_t cols, hi
       const dim3 grid((unsigned)cdiv(rows, RowGeom<L>::kRowsPerBlock));
       launch_timed(softmax_rows<T, L, VPT>, grid, dim3(RowGeom<L>::kThreads), 0, s, xp, yp, rows, (int)cols);
     });
+  }
+  if (!handled && cols > 4096 && cols <= 16 * kWideThreads) {
+    launch_timed(softmax_wide<T, 16>, dim3((unsigned)rows), dim3(kWideThreads), 0, s, xp, yp, (int)cols);
+    handled = true;
+  } else if (!handled && cols > 16 * kWideThreads && cols <= 64 * kWideThreads) {
+    launch_timed(softmax_wide<T, 64>, dim3((unsigned)rows), dim3(kWideThreads), 0, s, xp, yp, (int)cols);
+    handled = true;
   }
   if (!handled) launch_timed(softmax_loop<T>, dim3((unsigned)rows), dim3(kLoopThreads), 0, s, xp, yp, (int)cols);
   return record_launch();
@@ -331,6 +413,19 @@ __device__ __forceinline__ float ce_row_loss(const typename T::S* xr, int64_t t,
   if (t == ignore_index) return 0.f;
   if (t < 0 || t >= vocab) return NAN;
   const float lp = T::rnd(T::to_f(xr[t]) - M - logf(S));
+  return -lp;
+}
+
+// The same loss for a sum taken as s = sum 2^(x log2 e - mb), mb = round(M log2 e): the target's
+// exponent is formed the same way, so the rounding of mb (a factor 2^-eps in s) cancels in
+// lp = (x_t log2 e - mb) ln 2 - log s. Subtracting M directly would leave eps ln 2 in the loss
+// (5e-3 at |M| ~ 1e5).
+template <typename T>
+__device__ __forceinline__ float ce_row_loss_b2(const typename T::S* xr, int64_t t, int64_t vocab,
+                                                int64_t ignore_index, float mb, float s) {
+  if (t == ignore_index) return 0.f;
+  if (t < 0 || t >= vocab) return NAN;
+  const float lp = T::rnd(__builtin_fmaf(T::to_f(xr[t]), kLog2e, -mb) * kLn2 - logf(s));
   return -lp;
 }
 
@@ -362,7 +457,24 @@ __global__ __launch_bounds__(RowGeom<L>::kThreads) void ce_rows(
 #pragma unroll
       for (int e = 0; e < T::kVec; ++e) s += fast_exp2(__builtin_fmaf(r.f[j * T::kVec + e], kLog2e, -mb));
   s = group_reduce<L, 0>(s, red);
-  if (active && gl == 0) loss[row] = ce_row_loss<T>(x + row * cols, tgt[row], cols, ignore_index, m, s);
+  if (active && gl == 0) loss[row] = ce_row_loss_b2<T>(x + row * cols, tgt[row], cols, ignore_index, mb, s);
+}
+
+template <typename T, int EPT>
+__global__ __launch_bounds__(kWideThreads) void ce_wide(const typename T::S* __restrict__ x,
+                                                        const int64_t* __restrict__ tgt, float* __restrict__ loss,
+                                                        int cols, int64_t ignore_index) {
+  __shared__ float red[kWideThreads / kWave];
+  const typename T::S* xr = x + (int64_t)blockIdx.x * cols;
+  float v[EPT];
+  const float m = group_reduce<kWideThreads, 1>(wide_load_max<T, EPT>(xr, cols, v), red);
+  const float mb = m * kLog2e;
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < EPT; ++k)
+    if (threadIdx.x + k * kWideThreads < cols) s += fast_exp2(__builtin_fmaf(v[k], kLog2e, -mb));
+  s = group_reduce<kWideThreads, 0>(s, red);
+  if (threadIdx.x == 0) loss[blockIdx.x] = ce_row_loss_b2<T>(xr, tgt[blockIdx.x], cols, ignore_index, mb, s);
 }
 
 template <typename T>
@@ -411,6 +523,13 @@ static int launch_ce(const void* logits, const int64_t* tgt, float* loss, void* 
       const dim3 grid((unsigned)cdiv(rows, RowGeom<L>::kRowsPerBlock));
       ce_rows<T, L, VPT><<<grid, RowGeom<L>::kThreads, 0, s>>>(xp, tgt, loss, rows, (int)vocab, ignore_index);
     });
+  }
+  if (!handled && vocab > 4096 && vocab <= 16 * kWideThreads) {
+    ce_wide<T, 16><<<(unsigned)rows, kWideThreads, 0, s>>>(xp, tgt, loss, (int)vocab, ignore_index);
+    handled = true;
+  } else if (!handled && vocab > 16 * kWideThreads && vocab <= 64 * kWideThreads) {
+    ce_wide<T, 64><<<(unsigned)rows, kWideThreads, 0, s>>>(xp, tgt, loss, (int)vocab, ignore_index);
+    handled = true;
   }
   if (!handled) ce_loop<T><<<(unsigned)rows, kLoopThreads, 0, s>>>(xp, tgt, loss, (int)vocab, ignore_index);
   ce_mean<T><<<1, kMeanThreads, 0, s>>>(loss, tgt, (S*)out, rows, ignore_index);

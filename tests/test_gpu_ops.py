@@ -359,6 +359,42 @@ def test_softmax_dim_and_layernorm_none(gpu):
     assert_close(y, torch.nn.functional.layer_norm(x, (5,)), 1e-5, 1e-5, "layernorm no affine")
 
 
+WIDE_TOL = {torch.float16: 1e-3, torch.bfloat16: 2e-3, torch.float32: 1e-5}
+
+
+@pytest.mark.parametrize("cols", [4097, 16383, 16385, 50257, 65535, 65537])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=["f16", "bf16", "f32"])
+def test_softmax_ce_wide_odd_rows(gpu, cols, dtype):
+    """Widths that do not vectorise, on each side of the register-cached wide-row kernels' limits
+    (4096 < cols <= 16 * 1024 and <= 64 * 1024; 65537 stays on the looped kernel): softmax and
+    cross-entropy against the oracle, with a row holding -inf entries, a row of large values and a
+    constant row, and bitwise-equal reruns."""
+    g = torch.Generator().manual_seed(cols)
+    x = torch.randn(6, cols, generator=g) * 3
+    x[1, ::7] = -math.inf
+    x[2] = x[2] * 10 + (60000 if dtype == torch.float16 else 1e5)
+    x[3] = 0.5
+    x = x.to(dtype)
+    tol = WIDE_TOL[dtype]
+    sm = kernels.get("softmax")
+    y = sm(x.to(gpu))
+    assert_close(y, R.softmax_ref(x), tol, tol, f"softmax wide {cols} {dtype}")
+    assert torch.equal(y, sm(x.to(gpu))), "softmax wide rerun differs"
+    tg = torch.randint(0, cols, (6,), generator=g)
+    tg[1] = 7  # a -inf logit: loss +inf, as the oracle gives
+    tg[4] = -100
+    keep = [0, 2, 3, 5]
+    ce = kernels.get("cross_entropy")
+    out = ce(x[keep].to(gpu), tg[keep].to(gpu))
+    exp = R.cross_entropy_ref(x[keep], tg[keep])
+    ce_tol = 1e-5 if dtype == torch.float32 else 1e-2  # the op table's cross-entropy tolerances
+    assert abs(out.float().item() - exp.float().item()) <= ce_tol * max(1.0, abs(exp.float().item())), \
+        f"cross-entropy wide {cols} {dtype}: {out.float().item()} vs {exp.float().item()}"
+    out_inf = ce(x.to(gpu), tg.to(gpu))
+    assert math.isinf(out_inf.float().item()) and math.isinf(R.cross_entropy_ref(x, tg).float().item())
+    assert torch.equal(out, ce(x[keep].to(gpu), tg[keep].to(gpu))), "cross-entropy wide rerun differs"
+
+
 def test_cross_entropy_ignore_and_3d(gpu):
     g = torch.Generator().manual_seed(9)
     logits = torch.randn(2, 50, 320, generator=g).half()
