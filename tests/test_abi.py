@@ -72,7 +72,8 @@ def test_invalid_arguments_rejected_on_host(lib):
     assert lib.ak_gemm_residual(0, x, x, x, y, 4, 4, 4, 4, 4, 4, 0, None) == _lib.AK_EUNSUPPORTED  # fp32
     assert lib.ak_gemm_residual(1, x, x, x, y, 0, 4, 4, 4, 4, 4, 0, None) == _lib.AK_OK  # empty
     assert lib.ak_gemm_workspace_bytes(1, 1024, 1024, 8192, 8192, 8192, 1024, 1) == 4 * 1024 * 1024 * 4
-    assert lib.ak_gemm_workspace_bytes(1, 1024, 1024, 1024, 1024, 1024, 1024, 0) == 4 * 1024 * 1024 * 4
+    assert lib.ak_gemm_workspace_bytes(1, 1024, 1024, 4096, 4096, 1024, 1024, 0) == 4 * 1024 * 1024 * 4
+    assert lib.ak_gemm_workspace_bytes(1, 1024, 1024, 1024, 1024, 1024, 1024, 0) == 0   # slices < 1024 deep
     assert lib.ak_gemm_workspace_bytes(0, 1024, 1024, 8192, 8192, 8192, 1024, 1) == 0   # fp32: no split
     assert lib.ak_gemm_workspace_bytes(1, 4096, 4096, 4096, 4096, 4096, 4096, 1) == 0   # fills the GPU
     assert lib.ak_gemm_workspace_bytes(1, 1024, 1024, 8192, 8192, 8192, 1022, 1) == 0   # ldc % 4
