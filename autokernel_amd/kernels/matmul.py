@@ -10,10 +10,20 @@ fixed order).
 """
 from __future__ import annotations
 
+import functools
+
 import torch
 
 from .. import _lib
 from ._common import device_guard
+
+
+@functools.lru_cache(maxsize=1024)
+def _workspace_bytes(code: int, M: int, N: int, K: int, lda: int, ldb: int, ldc: int, bt: int) -> int:
+    """ak_gemm_workspace_bytes, remembered per argument tuple: the split decision depends on the
+    arguments alone, and a repeated shape then costs no library call."""
+    return _lib.load().ak_gemm_workspace_bytes(code, M, N, K, lda, ldb, ldc, bt)
+
 
 KERNEL_TYPE = "matmul"
 
@@ -65,7 +75,7 @@ def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, spli
     ldc = C.stride(0) if M > 1 else max(N, 1)
     with device_guard(A):
         # grids that leave most CUs idle split K over a torch-allocated fp32 workspace (ak_gemm_ws)
-        ws_bytes = lib.ak_gemm_workspace_bytes(code, M, N, K, lda, ldb, ldc, bt) if split_k else 0
+        ws_bytes = _workspace_bytes(code, M, N, K, lda, ldb, ldc, bt) if split_k else 0
         if ws_bytes > 0:
             ws = torch.empty(ws_bytes // 4, device=A.device, dtype=torch.float32)
             st = lib.ak_gemm_ws(code, A.data_ptr(), Bt.data_ptr(), C.data_ptr(), M, N, K, lda, ldb, ldc, bt,
