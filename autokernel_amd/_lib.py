@@ -45,7 +45,6 @@ SIGNATURES: dict[str, list] = {
     "ak_gemm_ws": [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p, _i64, _p],
     "ak_gemm_rope": [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p, _p, _i64, _i64, _i64, _p],
     "ak_mlp_gate_up": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i, _p],
-    "ak_transpose": [_i, _p, _p, _i64, _i64, _i64, _i64, _p],
     "ak_copy": [_p, _p, _i64, _p],
     "ak_set_launch_events": [_p, _p],
     "ak_flash_attn_fwd": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,

@@ -100,25 +100,5 @@ def _build(verbose, jobs, extra_flags, lib_path: Path, t0: float) -> Path:
     return lib_path
 
 
-PROBES = PKG_DIR / "probes"
-
-
-def build_probes(verbose: bool = True) -> list[Path]:
-    """Compile each standalone measurement program under probes/ (*.hip -> an executable beside
-    it): programs that time the hardware itself, not library code."""
-    built = []
-    for src in sorted(PROBES.glob("*.hip")):
-        exe = src.with_suffix("")
-        cmd = [hipcc(), *[f for f in HIP_FLAGS if f != "-fPIC"], str(src), "-o", str(exe)]
-        proc = subprocess.run(cmd, capture_output=True, text=True)
-        if proc.returncode != 0:
-            raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
-        built.append(exe)
-        if verbose:
-            print(f"built {exe}")
-    return built
-
-
 if __name__ == "__main__":
     build()
-    build_probes()

@@ -34,10 +34,7 @@ constexpr int kFaBKV = 64;   // keys per tile
 // accumulator is rescaled only a handful of times per row instead of on most tiles.
 constexpr float kFaRescaleSlack = 8.0f;
 
-#ifndef AK_FA_WAVES
-#define AK_FA_WAVES 4
-#endif
-constexpr int kFaWaves = AK_FA_WAVES;        // waves per block, 32 query rows each
+constexpr int kFaWaves = 4;                  // waves per block, 32 query rows each
 constexpr int kFaBQ = 32 * kFaWaves;         // query rows per block
 constexpr int kFaThreads = kFaWaves * 64;
 constexpr float kFaLog2e = 1.4426950408889634f;
@@ -411,17 +408,10 @@ __device__ __forceinline__ float fa2_halves_sum(float x) {
 }
 
 // fa_fwd2 work split: kFa2Waves waves of 32 query rows per block, two waves per SIMD.
-#ifndef AK_FA2_WAVES
-#define AK_FA2_WAVES 4
-#endif
-constexpr int kFa2Waves = AK_FA2_WAVES;
+constexpr int kFa2Waves = 4;
 constexpr int kFa2BQ = 32 * kFa2Waves;
 constexpr int kFa2Threads = 64 * kFa2Waves;
 constexpr int kFa2Layer = 256;  // blocks per layer: one per MI355X compute unit
-#ifndef AK_FA_SNAKE
-#define AK_FA_SNAKE 1
-#endif
-constexpr bool kFaSnake = AK_FA_SNAKE != 0;
 
 template <typename T, int D>
 __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
@@ -445,7 +435,7 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   // two blocks that share a CU pair a heavy and a light query block (measured [1, 32, 2048, 128]:
   // 56.2 -> 53.2 us; longer grids lose about 2 % with it). A bijection of block indices.
   int L = (int)blockIdx.x;
-  if (kFaSnake && causal && gridDim.x <= 2u * kFa2Layer) {
+  if (causal && gridDim.x <= 2u * kFa2Layer) {
     const int layer = L / kFa2Layer, base = layer * kFa2Layer;
     if (layer & 1) L = base + min(kFa2Layer, (int)gridDim.x - base) - 1 - (L - base);
   }

@@ -42,22 +42,17 @@ __device__ __forceinline__ f32x4 mfma16x16x32<TBF16>(const u32x4& a, const u32x4
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// The LDS-DMA kernel's MFMA in either shape: MF = 16 -> v_mfma_f32_16x16x32 (f32x4 accumulators),
-// MF = 32 -> v_mfma_f32_32x32x16 (f32x16). Both take 8 consecutive k of one row per lane.
+// The LDS-DMA kernel's MFMA: v_mfma_f32_16x16x32 (f32x4 accumulators), 8 consecutive k of one row
+// per lane. (32x32x16 fragments were measured 4-10 % slower on every workload.)
 template <int MF>
-struct MfmaAcc { using type = f32x4; };
-template <>
-struct MfmaAcc<32> { using type = f32x16; };
+struct MfmaAcc {
+  static_assert(MF == 16, "the LDS-DMA kernel uses 16x16x32 fragments");
+  using type = f32x4;
+};
 template <typename T, int MF>
 __device__ __forceinline__ typename MfmaAcc<MF>::type mfma_tile(const u32x4& a, const u32x4& b,
                                                                 const typename MfmaAcc<MF>::type& c) {
-  if constexpr (MF == 16) {
-    return mfma16x16x32<T>(a, b, c);
-  } else if constexpr (T::kCode == AK_F16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
+  return mfma16x16x32<T>(a, b, c);
 }
 
 // Load 8 consecutive k of one row of a K-contiguous matrix (row stride ld). Out-of-range rows or
@@ -514,10 +509,9 @@ __device__ __forceinline__ void gemm_dma_ns_kloop(
   constexpr int B_INS = GB::kRows / GB::RPI / NW;
   constexpr int INS = A_INS + NB * B_INS;
   constexpr int H = FM / 2;
-  constexpr int KS = MF == 16 ? 32 : 16;  // k per MFMA
+  constexpr int KS = 32;  // k per MFMA
   constexpr int STEPS = BKD / KS;         // k-steps per tile
   static_assert(NS >= 2 && NS <= 4, "stages");
-  static_assert(MF == 16 || !BKN, "[K, N] B fragments are built for the 16x16x32 shape");
   const uint16_t* Bm[2] = {B0, B1};
   // fragment row (lane % MF) and 16-byte k chunk (lane / MF) of this lane
   const int fr = lane & (MF - 1), fc = lane / MF;
@@ -692,27 +686,9 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
   gemm_dma_ns_kloop<T, BM, BN, WM, WN, NB, BKD, NS, BKN, MF>(acc, A, B0, B1, oa, ob, kb_step_b, K, wid, wm, wn,
                                                              lane, sS0, sS1, sS2, sS3);
 
-  if constexpr (MF == 16) {
-    // 16x16 fragment: lane holds C[m0' + lane % 16][n0' + 4 (lane / 16) + 0..3]
-    const int fr = lane & 15, fc = lane >> 4;
-    tile_epilogue<T, NB, EPI, true, FM, FN>(C, B1, ldc, M, N, m0 + wm * WTM + fr, n0 + wn * WTN + fc * 4, acc, ep);
-  } else {
-    // 32x32 fragment: lane holds C[m0' + lane % 32][n0' + 8 g + 4 (lane / 32) + 0..3], g = 0..3,
-    // in accumulator elements 4 g .. 4 g + 3: four 4-column groups 8 columns apart
-    f32x4 acc4[NB][FM][FN * 4];
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-          for (int g = 0; g < 4; ++g)
-            acc4[b][i][4 * j + g] = f32x4{acc[b][i][j][4 * g], acc[b][i][j][4 * g + 1], acc[b][i][j][4 * g + 2],
-                                          acc[b][i][j][4 * g + 3]};
-    tile_epilogue<T, NB, EPI, true, FM, FN * 4, 32, 8>(C, B1, ldc, M, N, m0 + wm * WTM + (lane & 31),
-                                                       n0 + wn * WTN + 4 * (lane >> 5), acc4, ep);
-  }
+  // 16x16 fragment: lane holds C[m0' + lane % 16][n0' + 4 (lane / 16) + 0..3]
+  const int fr = lane & 15, fc = lane >> 4;
+  tile_epilogue<T, NB, EPI, true, FM, FN>(C, B1, ldc, M, N, m0 + wm * WTM + fr, n0 + wn * WTN + fc * 4, acc, ep);
 }
 
 // --------------------------------------------------------------------------------------------
@@ -842,19 +818,13 @@ struct TileCfg {
 
 // Pick the tile that keeps the 256 CUs busiest: fraction of CU-slots doing useful work over the
 // launch, weighted by the per-tile efficiency of smaller tiles (more LDS and L2 traffic per flop).
-#ifndef AK_GEMM_EFF256
-#define AK_GEMM_EFF256 1.0
-#endif
-#ifndef AK_GEMM_EFF192
-#define AK_GEMM_EFF192 0.88
-#endif
 // wide192: also consider 256x192 tiles (the LDS-DMA kernel with nn.Linear-layout B; 2048 x 6144,
 // a fused QKV projection, is then exactly one tile per CU)
 static TileCfg pick_tile(int64_t M, int64_t N, int nb, bool wide192 = false) {
   const TileCfg cands[] = {{256, 256}, {256, 128}, {128, 128}, {256, 192}};
   // relative per-flop throughput of the tiles (bf16, MI355X): 4096^3 on 256x256 1230 TF/s,
   // 2048x4096x4096 on 256x128 1084 TF/s, 2048x6144x4096 on 128x128 786 TF/s, on 256x192 1108 TF/s
-  const double eff[] = {AK_GEMM_EFF256, 0.88, 0.64, AK_GEMM_EFF192};
+  const double eff[] = {1.0, 0.88, 0.64, 0.88};
   const int cus = 256;
   TileCfg best = cands[2];
   double best_s = -1.0;
@@ -884,12 +854,9 @@ static void launch_gemm_cfg(const void* A, const void* B0, const void* B1, void*
       ldc, tiles_m, tiles_n, ep);
 }
 
-// Waves along N of the 256x256 tile: 4 (8 waves of 128x64) or 2 (4 waves of 128x128, one wave
-// per SIMD, accumulators in AGPRs).
-#ifndef AK_GEMM_BIG_WN
-#define AK_GEMM_BIG_WN 4
-#endif
-constexpr int kBigWN = AK_GEMM_BIG_WN;
+// Waves along N of the 256x256 tile: 4 (8 waves of 128x64; measured faster than 4 waves of
+// 128x128, one wave per SIMD with accumulators in AGPRs).
+constexpr int kBigWN = 4;
 
 template <typename T, bool BT, bool VEC, int NB, int EPI>
 static void launch_gemm_tiled(const void* A, const void* B0, const void* B1, void* C, int M, int N,
@@ -912,29 +879,14 @@ static void launch_gemm_tiled(const void* A, const void* B0, const void* B1, voi
   }
 }
 
-#ifndef AK_GEMM_DMA
-#define AK_GEMM_DMA 1
-#endif
-constexpr bool kUseDma = AK_GEMM_DMA != 0;
-#ifndef AK_GEMM_DEEP
-#define AK_GEMM_DEEP 1
-#endif
-constexpr bool kUseDeep = AK_GEMM_DEEP != 0;
 constexpr int kCUs = 256;  // MI355X compute units
-
-#ifndef AK_GEMM_MF
-#define AK_GEMM_MF 16
-#endif
-constexpr int kGemmMF = AK_GEMM_MF;
 
 template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, int BKD, int NS, bool BKN>
 static void launch_dma_kernel(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
                               int64_t lda, int64_t ldb, int64_t ldc, int tiles_m, int tiles_n, hipStream_t s,
                               const EpiArgs& ep) {
-  // MFMA shape: 32x32x16 where the wave tile holds whole 32x32 fragments (an even count along M)
-  // and B is nn.Linear-layout; else 16x16x32
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int MF = (kGemmMF == 32 && !BKN && WTN % 32 == 0 && (WTM / 32) % 2 == 0) ? 32 : 16;
+  // MFMA shape 16x16x32 (32x32x16 fragments measured 4-10 % slower on every workload)
+  constexpr int MF = 16;
   gemm_dma<T, BM, BN, WM, WN, NB, EPI, BKD, NS, BKN, MF><<<dim3(tiles_m * tiles_n, ep.splits), WM * WN * kWave, 0, s>>>(
       (const uint16_t*)A, (const uint16_t*)B0, (const uint16_t*)B1, (uint16_t*)C, M, N, K, lda, ldb, ldc,
       tiles_m, tiles_n, ep);
@@ -942,36 +894,23 @@ static void launch_dma_kernel(const void* A, const void* B0, const void* B1, voi
 
 // Pipeline plan per tile shape: stage bytes (BM + NB * BN) * BKD * 2 and the 160 KB of LDS fix
 // how many stages fit.
-#ifndef AK_GEMM_PLAN
-#define AK_GEMM_PLAN 2
-#endif
-// Waves along N of the 128x128 tile: 4 (8 waves of 64x32, two per SIMD) or 2 (4 waves of 64x64,
-// one per SIMD). Measured, cold, 2048^3 (256 tiles, one per CU): f16 NN 26.8 us with 8 waves against
-// 36.5 us with 4 (stock hipBLASLt 32.0), bf16 NT 26.4 against 36.0 (28.9); three or four stages for
-// the 4-wave tile reach 28.2-29.4 us. Shapes on other tiles are unchanged.
-#ifndef AK_GEMM_SMALL_WN
-#define AK_GEMM_SMALL_WN 4
-#endif
-constexpr int kSmallWN = AK_GEMM_SMALL_WN;
-// stages for 4-wave tiles under plan 2: 2, or up to this many where they fit
-#ifndef AK_GEMM_NS4
-#define AK_GEMM_NS4 2
-#endif
+// Waves along N of the 128x128 tile: 4 (8 waves of 64x32, two per SIMD). Measured, cold, 2048^3
+// (256 tiles, one per CU): f16 NN 26.8 us against 36.5 us with 4 waves of 64x64 (stock hipBLASLt
+// 32.0), bf16 NT 26.4 against 36.0 (28.9); three or four stages for the 4-wave tile reach
+// 28.2-29.4 us. Shapes on other tiles are unchanged.
+constexpr int kSmallWN = 4;
 
 template <int BM, int BN, int NB, int NW>
 struct DmaPlan {
   static constexpr int kStage64 = (BM + NB * BN) * 64 * 2;
   static constexpr int kFit64 = 163840 / kStage64;
   static constexpr bool kOk32 = BM % (16 * NW) == 0 && BN % (16 * NW) == 0;
-  // plan 1: two 64-deep stages; 2 (default): three 64-deep stages where they fit beside 8 waves,
-  // else two; 3: four 32-deep stages. Measured (bf16, NT):
+  // Three 64-deep stages where they fit beside 8 waves, else two. Measured (bf16, NT):
   // 2048x4096x4096 on 256x128 tiles 83.5 us two-stage -> 63.4 us three-stage; 4096^3 on 256x256
-  // 107.4 us two-stage (plan 3: 121.2 us, the doubled barrier count outweighs the deeper queue).
-  static constexpr int BKD = (AK_GEMM_PLAN == 3 && kOk32) ? 32 : 64;
-  static constexpr int NS = AK_GEMM_PLAN == 1 ? 2
-                            : AK_GEMM_PLAN == 2 ? (kFit64 >= 3 && NW == 8 ? 3
-                                                   : (NW == 4 ? (kFit64 < AK_GEMM_NS4 ? kFit64 : AK_GEMM_NS4) : 2))
-                            : (kOk32 ? 4 : 2);
+  // 107.4 us two-stage (four 32-deep stages: 121.2 us, the doubled barrier count outweighs the
+  // deeper queue).
+  static constexpr int BKD = 64;
+  static constexpr int NS = (kFit64 >= 3 && NW == 8) ? 3 : 2;
 };
 
 template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, bool BKN>
@@ -984,7 +923,7 @@ static void launch_dma_cfg(const void* A, const void* B0, const void* B1, void* 
   // 64-deep pair is faster per tile (2048x6144x4096 on 192 tiles of 256x256: 109.9 us against
   // 127.5 us).
   constexpr bool kOk32 = P::kOk32;
-  if (kOk32 && kUseDeep && 2 * tiles_m * tiles_n * ep.splits <= kCUs) {
+  if (kOk32 && 2 * tiles_m * tiles_n * ep.splits <= kCUs) {
     if constexpr (kOk32)
       launch_dma_kernel<T, BM, BN, WM, WN, NB, EPI, 32, 4, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, tiles_m,
                                                                 tiles_n, s, ep);
@@ -1029,14 +968,14 @@ static int launch_gemm16(const void* A, const void* B0, const void* B1, void* C,
   const int m = (int)M, n = (int)N, k = (int)K;
   // LDS-DMA path: nn.Linear-layout B, K a multiple of 64, 32-bit element offsets
   const bool fits32 = M * lda < INT_MAX && N * ldb < INT_MAX;
-  if (bt && vec && K % kBK == 0 && K > 0 && fits32 && kUseDma) {
+  if (bt && vec && K % kBK == 0 && K > 0 && fits32) {
     launch_gemm_dma<T, NB, EPI, false>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s, ep);
     return record_launch();
   }
   // [K, N] B (torch.matmul's layout) on the same pipeline, fragments read through LDS transposes
   if constexpr (NB == 1) {
     const bool fits32_kn = M * lda < INT_MAX && K * ldb < INT_MAX;
-    if (!bt && vec && K % kBK == 0 && K > 0 && N >= 8 && fits32_kn && kUseDma) {
+    if (!bt && vec && K % kBK == 0 && K > 0 && N >= 8 && fits32_kn) {
       launch_gemm_dma<T, 1, EPI, true>(A, B0, B1, C, m, n, k, lda, ldb, ldc, s, ep);
       return record_launch();
     }
@@ -1088,7 +1027,9 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
 static int splitk_slices(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, bool bt) {
   if (M <= 0 || N <= 0 || K <= 0 || N % 4 != 0 || ldc % 4 != 0 || lda % 8 != 0 || ldb % 8 != 0) return 1;
   if (M * lda >= INT_MAX || (bt ? N : K) * ldb >= INT_MAX || M * N * 8 >= INT_MAX) return 1;
-  if (!bt && N < 8) return 1;
+  // [K, N] B runs the LDS-DMA kernel only with N a multiple of 8 (its 16-byte column chunks), the
+  // same rule as the unsplit path
+  if (!bt && N % 8 != 0) return 1;
   const TileCfg t = pick_tile(M, N, 1, !bt);
   const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
   if (2 * tiles > kCUs) return 1;

@@ -5,9 +5,8 @@
 //   y[2i+1] = rnd(rnd(x[2i]*sin[i]) + rnd(x[2i+1]*cos[i]))
 // rnd() rounds to the element type, as each elementwise tensor op of the reference does; for
 // fp32 no fused multiply-add is formed, so every element is bit-identical to the tensor ops.
-// The fast path moves 16-byte vectors of x (4 pairs for f16 / bf16) with two 8-byte table slices
-// each, four vectors per thread with all loads issued first; table rows stay hot in L2 across
-// heads.
+// The fast path moves one 16-byte vector of x (4 pairs for f16 / bf16) per thread with two 8-byte
+// table slices; table rows stay hot in L2 across heads.
 #include <limits.h>
 
 #include "ak_common.h"
@@ -20,13 +19,6 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
   *y1 = T::rnd(T::rnd(x1 * c) - T::rnd(x2 * s));
   *y2 = T::rnd(T::rnd(x1 * s) + T::rnd(x2 * c));
 }
-
-// Each thread rotates kCpt 16-byte chunks spaced one grid apart, issuing all loads before any
-// arithmetic so a wave keeps kCpt x 1 KB of x in flight.
-#ifndef AK_ROPE_CPT
-#define AK_ROPE_CPT 1
-#endif
-constexpr int kRopeCpt = AK_ROPE_CPT;
 
 template <typename T>
 __device__ __forceinline__ u32x4 rope_chunk(const u32x4& xv, const typename T::S* cp, const typename T::S* sp) {
@@ -67,24 +59,13 @@ __global__ __launch_bounds__(256) void rope_vec(const typename T::S* __restrict_
                                                 int chunks_per_row, int half, int64_t table_rows,
                                                 int64_t rep_inner) {
   constexpr int kP = T::kVec / 2;
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  const int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  u32x4 xv[kRopeCpt];
-#pragma unroll
-  for (int u = 0; u < kRopeCpt; ++u) {
-    const int64_t i = i0 + u * stride;
-    if (i < nchunks) xv[u] = ld16(x + i * T::kVec);
-  }
-#pragma unroll
-  for (int u = 0; u < kRopeCpt; ++u) {
-    const int64_t i = i0 + u * stride;
-    if (i < nchunks) {
-      const int64_t row = i / chunks_per_row;
-      const int c = (int)(i - row * chunks_per_row);
-      const int64_t trow = (row / rep_inner) % table_rows;
-      st16(y + i * T::kVec, rope_chunk<T>(xv[u], ct + trow * half + c * kP, st + trow * half + c * kP));
-    }
-  }
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nchunks) return;
+  const u32x4 xv = ld16(x + i * T::kVec);
+  const int64_t row = i / chunks_per_row;
+  const int c = (int)(i - row * chunks_per_row);
+  const int64_t trow = (row / rep_inner) % table_rows;
+  st16(y + i * T::kVec, rope_chunk<T>(xv, ct + trow * half + c * kP, st + trow * half + c * kP));
 }
 
 // Any alignment: one pair per thread.
@@ -150,7 +131,7 @@ static int launch_rope(const void* x, const void* c, const void* s, void* y, int
   if (vec) {
     const int cpr = (int)(d / T::kVec);
     const int64_t n = rows * cpr;
-    rope_vec<T><<<(unsigned)cdiv(n, 256 * kRopeCpt), 256, 0, stream>>>(
+    rope_vec<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>(
         (const S*)x, (const S*)c, (const S*)s, (S*)y, n, cpr, half, table_rows, rep_inner);
   } else {
     const int64_t n = rows * half;

@@ -39,18 +39,6 @@ def _b_layout(B: torch.Tensor) -> tuple[torch.Tensor, int, int]:
     return Bc, max(N, 1), 0
 
 
-def transpose(B: torch.Tensor) -> torch.Tensor:
-    """Contiguous B.T of a row-major 2-D tensor via ak_transpose."""
-    K, N = B.shape
-    out = torch.empty((N, K), device=B.device, dtype=B.dtype)
-    code = _lib.dtype_code(B, "transpose")
-    with device_guard(B):
-        st = _lib.load().ak_transpose(code, B.data_ptr(), out.data_ptr(), K, N, B.stride(0), max(K, 1),
-                                      _lib.stream_of(B))
-    _lib.check(st, "ak_transpose", shape=tuple(B.shape), dtype=B.dtype)
-    return out
-
-
 def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, split_k: bool = False) -> torch.Tensor:
     """C = A @ B for 2-D A [M, K] and 2-D B [K, N] (B may be a transposed [N, K] view).
 

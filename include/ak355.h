@@ -200,14 +200,6 @@ int ak_gemm_rope(int dtype, const void* A, const void* B, void* C, int64_t M, in
                  hipStream_t stream);
 
 /*
- * 2-D transpose: dst[c][r] = src[r][c] for a rows x cols matrix with row strides ld_src / ld_dst.
- * No counterpart in the reference: a layout helper for callers that keep a transposed copy of a
- * matrix (ak_gemm itself reads both B layouts in place).
- */
-int ak_transpose(int dtype, const void* src, void* dst, int64_t rows, int64_t cols,
-                 int64_t ld_src, int64_t ld_dst, hipStream_t stream);
-
-/*
  * Device copy of `bytes` bytes (a multiple of 16, 16-byte aligned src and dst), one 16-byte vector
  * per thread. No counterpart in the reference: the bandwidth reference the benchmark times beside
  * the HBM-bound ops (the practical ceiling at a given size).

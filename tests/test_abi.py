@@ -77,6 +77,9 @@ def test_invalid_arguments_rejected_on_host(lib):
     assert lib.ak_gemm_workspace_bytes(0, 1024, 1024, 8192, 8192, 8192, 1024, 1) == 0   # fp32: no split
     assert lib.ak_gemm_workspace_bytes(1, 4096, 4096, 4096, 4096, 4096, 4096, 1) == 0   # fills the GPU
     assert lib.ak_gemm_workspace_bytes(1, 1024, 1024, 8192, 8192, 8192, 1022, 1) == 0   # ldc % 4
+    # [K, N] B with N % 8 == 4 (a padded column slice): the [K, N] split kernel needs N % 8 == 0
+    assert lib.ak_gemm_workspace_bytes(1, 1024, 1020, 4096, 4096, 1024, 1020, 0) == 0
+    assert lib.ak_gemm_workspace_bytes(1, 1024, 1020, 4096, 4096, 4096, 1020, 1) > 0   # [N, K] B splits
     assert lib.ak_gemm_ws(1, x, x, x, 0, 4, 4, 4, 4, 4, 1, None, 0, None) == _lib.AK_OK  # empty -> ak_gemm
     rope = lib.ak_gemm_rope
     assert rope(1, x, x, y, 4, 8, 4, 4, 4, 8, 1, x, x, 4, 6, 6, None) == _lib.AK_EINVAL  # head_dim % 4

@@ -416,18 +416,6 @@ def test_fused_mlp_activations_f16(gpu):
         assert_close(out, R.fused_mlp_ref(x, wg, wu, wd, act), 1e-2, 1e-2, f"mlp {act}")
 
 
-def test_transpose_layout_helper(gpu):
-    from autokernel_amd.kernels.matmul import transpose
-    g = torch.Generator().manual_seed(11)
-    for (r, c) in ((64, 64), (4096, 4096), (1023, 1537), (7, 300), (300, 7)):
-        for dt in (torch.float16, torch.bfloat16, torch.float32):
-            x = torch.randn(r, c, generator=g).to(dt)
-            assert torch.equal(transpose(x.to(gpu)).cpu(), x.t().contiguous()), (r, c, dt)
-    big = torch.randn(128, 200, generator=g).half()
-    view = big.to(gpu)[:, 8:136]  # row stride 200
-    assert torch.equal(transpose(view).cpu(), big[:, 8:136].t().contiguous())
-
-
 def test_copy_reference_kernel(gpu):
     """ak_copy (the bandwidth reference of the benchmark) copies bytes exactly, odd sizes included."""
     from autokernel_amd import _lib
@@ -602,3 +590,22 @@ def test_gemm_split_k(gpu, M, N, K, bt):
         outs = [gemm(A.to(gpu), Bd, split_k=True) for _ in range(3)]
         assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
         assert_close(outs[0], R.matmul_ref(A.float(), W.float().T).to(dt), 2e-2, 2e-2, f"split {M}x{N}x{K} {dt}")
+
+
+@pytest.mark.parametrize("N", [1020, 1004])
+def test_gemm_padded_kn_view_not_split(gpu, N):
+    """A [K, N] B that is a column slice of a wider matrix (N % 8 == 4, ldb % 8 == 0, long K) must not
+    take the split path, whose [K, N] kernel needs N % 8 == 0: the result equals the oracle in
+    every column, the last four included."""
+    from autokernel_amd import _lib
+    from autokernel_amd.kernels.matmul import gemm
+    lib = _lib.load()
+    M, K, ld = 1024, 4096, 1024
+    g = torch.Generator().manual_seed(N)
+    A = (torch.randn(M, K, generator=g) / K ** 0.5).half()
+    Bfull = torch.randn(K, ld, generator=g).half()
+    assert lib.ak_gemm_workspace_bytes(_lib.AK_F16, M, N, K, K, ld, N, 0) == 0
+    out = gemm(A.to(gpu), Bfull.to(gpu)[:, :N], split_k=True)
+    exp = R.matmul_ref(A.float(), Bfull[:, :N].float()).half()
+    assert_close(out, exp, 1e-2, 1e-2, f"padded [K, N] view N={N}")
+    assert_close(out[:, -4:], exp[:, -4:], 1e-2, 1e-2, "last four columns")
