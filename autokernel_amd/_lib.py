@@ -21,6 +21,7 @@ DTYPE_CODE = {torch.float32: AK_F32, torch.float16: AK_F16, torch.bfloat16: AK_B
 AK_OK, AK_EINVAL, AK_EUNSUPPORTED, AK_EHIP = 0, 1, 2, 3
 ACTIVATIONS = {"silu": 0, "gelu": 1, "relu2": 2}
 ACT_NONE = 3
+CE_NOALLOC_MAX_ROWS = 1 << 20  # AK_CE_NOALLOC_MAX_ROWS (include/ak355.h)
 
 _i = ctypes.c_int
 _i64 = ctypes.c_int64
@@ -37,6 +38,7 @@ SIGNATURES: dict[str, list] = {
     "ak_rope_f32_tables": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
     "ak_rmsnorm_rsqrt": [_i, _p, _p, _p, _i64, _i64, _f, _p],
     "ak_cross_entropy": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _p],
+    "ak_cross_entropy_noalloc": [_i, _p, _p, _p, _i64, _i64, _i64, _p],
     "ak_reduce_sum": [_i, _p, _p, _i64, _i64, _i64, _p],
     "ak_reduce_max": [_i, _p, _p, _i64, _i64, _i64, _p],
     "ak_gemm": [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],

@@ -184,6 +184,7 @@ __device__ __forceinline__ bool aligned16(const void* p) { return (((uintptr_t)p
 // Host-side helpers
 // ---------------------------------------------------------------------------------------------
 int record_launch(void);  // checks hipGetLastError(), stores its text, returns AK_OK / AK_EHIP
+int record_hip_error(hipError_t e);  // AK_OK for hipSuccess, else stores e's text and returns AK_EHIP
 
 // Start / stop events set by ak_set_launch_events for the calling thread's next timed launch
 // (null when none); taking them clears the slot.

@@ -14,8 +14,9 @@ LaunchEvents take_launch_events(void) {
   return e;
 }
 
-int record_launch(void) {
-  const hipError_t e = hipGetLastError();
+int record_launch(void) { return record_hip_error(hipGetLastError()); }
+
+int record_hip_error(hipError_t e) {
   if (e == hipSuccess) return AK_OK;
   snprintf(g_last_error, sizeof(g_last_error), "%s (%d): %s", hipGetErrorName(e), (int)e,
            hipGetErrorString(e));

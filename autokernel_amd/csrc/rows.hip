@@ -3,6 +3,9 @@
 // and written once; reductions are wave64 butterflies plus a fixed-order LDS combine.
 #include <limits.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "row_common.h"
 
 namespace ak {
@@ -669,6 +672,67 @@ extern "C" int ak_cross_entropy(int dtype, const void* logits, const int64_t* ta
   if (!out) return AK_EINVAL;
   if (rows > 0 && (!logits || !targets || !row_loss || vocab == 0)) return AK_EINVAL;
   AK_DISPATCH(dtype, T, return launch_ce<T>(logits, targets, row_loss, out, rows, vocab, ignore_index, stream));
+}
+
+// ---------------------------------------------------------------------------------------------
+// ak_cross_entropy_noalloc: ak_cross_entropy with the per-row losses in a file-scope device array
+// instead of a caller workspace, for callers that cannot allocate. In host code `scratch` names a
+// host-side stand-in, not device memory: its device address is looked up once per device with
+// hipGetSymbolAddress (that device current) and cached; kernels only ever get that address.
+// Every call writes the loss of each of its rows before ce_mean reads it, so nothing has to be
+// cleared between calls; calls that overlap on one device share the array and race.
+// ---------------------------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[AK_CE_NOALLOC_MAX_ROWS];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<float*> g_scratch[kMaxDevices];
+
+// Device address of `scratch` on the device that runs `stream` (the current device for the null
+// stream); AK_OK or an error status.
+int ce_scratch(hipStream_t stream, float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess && stream) e = hipStreamGetDevice(stream, &dev);
+  if (e != hipSuccess) return record_hip_error(e);
+  if (dev < 0 || dev >= kMaxDevices) return AK_EUNSUPPORTED;
+  float* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      int cur = dev;
+      e = hipGetDevice(&cur);
+      if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+      void* addr = nullptr;
+      if (e == hipSuccess) e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (cur != dev) {
+        const hipError_t e2 = hipSetDevice(cur);
+        if (e == hipSuccess) e = e2;
+      }
+      if (e != hipSuccess) return record_hip_error(e);
+      if (!addr) return AK_EHIP;
+      p = static_cast<float*>(addr);
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return AK_OK;
+}
+}  // namespace
+
+extern "C" int ak_cross_entropy_noalloc(int dtype, const void* logits, const int64_t* targets, void* out,
+                                        int64_t rows, int64_t vocab, int64_t ignore_index, hipStream_t stream) {
+  if (bad_rows(rows, vocab)) return AK_EINVAL;
+  if (rows > AK_CE_NOALLOC_MAX_ROWS) return AK_EINVAL;
+  if (!out) return AK_EINVAL;
+  if (rows > 0 && (!logits || !targets || vocab == 0)) return AK_EINVAL;
+  if (dtype != AK_F32 && dtype != AK_F16 && dtype != AK_BF16) return AK_EINVAL;
+  float* loss = nullptr;
+  const int st = ce_scratch(stream, &loss);
+  if (st != AK_OK) return st;
+  AK_DISPATCH(dtype, T, return launch_ce<T>(logits, targets, loss, out, rows, vocab, ignore_index, stream));
 }
 
 extern "C" int ak_reduce_sum(int dtype, const void* x, void* y, int64_t outer, int64_t reduce,

@@ -4,9 +4,11 @@
  * Every entry point:
  *   - takes device pointers, element counts and scalars only (no framework types);
  *   - launches asynchronously on the caller's HIP stream `stream` (pass torch's current stream);
- *   - never allocates, frees or synchronises; every buffer (outputs, workspaces) is the caller's;
+ *   - never allocates, frees or synchronises; every buffer (outputs, workspaces) is the caller's
+ *     (ak_cross_entropy_noalloc alone keeps its workspace in a fixed device array, see there);
  *   - keeps no mutable global state, so concurrent calls on different streams are safe (the
- *     one per-thread setting, ak_set_launch_events, affects only its own thread's next launch);
+ *     one per-thread setting, ak_set_launch_events, affects only its own thread's next launch;
+ *     ak_cross_entropy_noalloc's calls on one device share its array);
  *   - returns AK_OK or an ak_status code; AK_EHIP means a HIP launch error
  *     (its text is available from ak_last_hip_error_string() on the calling thread).
  *
@@ -129,6 +131,20 @@ int ak_rope_f32_tables(int dtype, const void* x, const float* cos_t, const float
 int ak_cross_entropy(int dtype, const void* logits, const int64_t* targets, float* row_loss,
                      void* out, int64_t rows, int64_t vocab, int64_t ignore_index,
                      hipStream_t stream);
+
+/*
+ * Cross-entropy that allocates nothing: the result of ak_cross_entropy (same arguments except the
+ * row_loss workspace, same kernels, bit-identical output), with the per-row losses kept in a
+ * fixed device array of AK_CE_NOALLOC_MAX_ROWS floats (4 MiB) that the library holds on each
+ * device it runs on until the process ends. rows above AK_CE_NOALLOC_MAX_ROWS: AK_EINVAL.
+ * Calls that overlap on one device (concurrent streams or threads) share that array and race:
+ * serialise them. The device is the stream's (the current device for the null stream).
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ */
+#define AK_CE_NOALLOC_MAX_ROWS (1 << 20)
+int ak_cross_entropy_noalloc(int dtype, const void* logits, const int64_t* targets, void* out,
+                             int64_t rows, int64_t vocab, int64_t ignore_index, hipStream_t stream);
 
 /*
  * Sum / max over the middle dim of x viewed as [outer, reduce, inner]; y: [outer, inner].

@@ -80,6 +80,11 @@ def test_invalid_arguments_rejected_on_host(lib):
     # [K, N] B with N % 8 == 4 (a padded column slice): the [K, N] split kernel needs N % 8 == 0
     assert lib.ak_gemm_workspace_bytes(1, 1024, 1020, 4096, 4096, 1024, 1020, 0) == 0
     assert lib.ak_gemm_workspace_bytes(1, 1024, 1020, 4096, 4096, 4096, 1020, 1) > 0   # [N, K] B splits
+    # the no-alloc cross-entropy refuses more rows than its device array holds, before any HIP call
+    big = _lib.CE_NOALLOC_MAX_ROWS + 1
+    assert lib.ak_cross_entropy_noalloc(1, x, x, x, big, 8, -100, None) == _lib.AK_EINVAL
+    assert lib.ak_cross_entropy_noalloc(1, x, x, None, 4, 8, -100, None) == _lib.AK_EINVAL   # no output
+    assert lib.ak_cross_entropy_noalloc(7, x, x, x, 4, 8, -100, None) == _lib.AK_EINVAL      # bad dtype
     assert lib.ak_gemm_ws(1, x, x, x, 0, 4, 4, 4, 4, 4, 1, None, 0, None) == _lib.AK_OK  # empty -> ak_gemm
     rope = lib.ak_gemm_rope
     assert rope(1, x, x, y, 4, 8, 4, 4, 4, 8, 1, x, x, 4, 6, 6, None) == _lib.AK_EINVAL  # head_dim % 4
