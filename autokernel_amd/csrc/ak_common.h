@@ -85,10 +85,7 @@ struct TBF16 {
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
-// Streaming variants: data touched once, keep it out of the way of reused data.
-__device__ __forceinline__ u32x4 ld16_stream(const void* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-}
+// Nontemporal store: data written once and not read back soon.
 __device__ __forceinline__ void st16_stream(void* p, const u32x4& v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }

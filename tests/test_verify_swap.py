@@ -134,3 +134,117 @@ def test_fused_qkv_causal_attention_strategy():
         assert not isinstance(m[1], verify.FusedQKVAttentionWrapper), "a non-causal mask must not be swapped"
         assert ctx.applied == {"attention": 1, "matmul": 2}, ctx.applied
     assert {n: type(x) for n, x in m.named_modules()} == before
+
+
+# ------------------------------------------------------------------ external kernel modules
+FAKE_LN = '''
+import torch
+KERNEL_TYPE = "layernorm"
+CALLS = []
+def kernel_fn(x, weight, bias, eps=1e-5):
+    CALLS.append(tuple(x.shape))
+    return torch.nn.functional.layer_norm(x, x.shape[-1:], weight, bias, eps)
+'''
+FAKE_MM = '''
+import torch
+KERNEL_TYPE = "matmul"
+def kernel_fn(A, B):
+    assert B.is_contiguous()          # the reference hands over weight.t().contiguous()
+    return A @ B
+'''
+FAKE_RMS_NO_EPS = '''
+import torch
+def kernel_fn(x, weight):             # no eps parameter: the wrapper's TypeError fallback
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * weight
+'''
+
+
+def _write(d, name, text):
+    p = d / name
+    p.write_text(text)
+    return str(p)
+
+
+def test_discovery_by_file_name(tmp_path):
+    for n in ("kernel_flash_attention_1_optimized.py", "kernel_matmul_12_optimized.py",
+              "kernel_layernorm_3_optimized.py", "notes.py", "kernel_x_optimized.py"):
+        _write(tmp_path, n, "def kernel_fn(*a):\n    return None\n")
+    found = verify.discover_optimized_kernels(str(tmp_path))
+    got = [(r.kernel_type, r.rank, r.speedup) for r in found]
+    assert got == [("flash_attention", 1, 0.0), ("layernorm", 3, 0.0), ("matmul", 12, 0.0)]
+
+
+def test_discovery_from_orchestration_state(tmp_path):
+    import json
+    _write(tmp_path, "kernel_matmul_1_optimized.py", FAKE_MM)
+    _write(tmp_path, "op7_optimized.py", FAKE_LN)
+    _write(tmp_path, "kernel_rmsnorm_2_optimized.py", FAKE_RMS_NO_EPS)
+    state = {"kernels": [
+        {"op_type": "matmul", "rank": 1, "speedup": 1.8},                       # conventional name
+        {"type": "layernorm", "rank": 4, "best_speedup": 1.2, "file": "k/op7.py"},  # from "file"
+        {"op_type": "rmsnorm", "rank": 2, "speedup": 0.9},                      # no speedup: dropped
+        {"op_type": "softmax", "rank": 3, "speedup": 2.0},                      # file missing: dropped
+    ]}
+    (tmp_path / "orchestration_state.json").write_text(json.dumps(state))
+    found = verify.discover_optimized_kernels(str(tmp_path))
+    assert [(r.kernel_type, r.rank, r.speedup) for r in found] == [("matmul", 1, 1.8), ("layernorm", 4, 1.2)]
+    assert found[1].optimized_path.endswith("op7_optimized.py")
+
+
+def test_external_modules_swap_and_restore(tmp_path):
+    """External kernel_fns replace nn.Linear / nn.LayerNorm / RMSNorm modules with the reference's
+    call conventions; the forward equals stock; everything is restored on exit."""
+    import torch
+    ln = _write(tmp_path, "kernel_layernorm_1_optimized.py", FAKE_LN)
+    mm = _write(tmp_path, "kernel_matmul_2_optimized.py", FAKE_MM)
+    rms = _write(tmp_path, "kernel_rmsnorm_3_optimized.py", FAKE_RMS_NO_EPS)
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Linear(16, 32), nn.LayerNorm(32), nn.Linear(32, 8, bias=False),
+                          llama.RMSNorm(8)).eval()
+    x = torch.randn(3, 5, 16)
+    with torch.no_grad():
+        ref = model(x)
+    before = {n: type(m) for n, m in model.named_modules()}
+    reps = [verify.replacement_from_module(p) for p in (ln, mm)] + verify.discover_optimized_kernels(str(tmp_path))[2:]
+    ctx = verify.OptimizedModelContext(model, reps)
+    with ctx as m, torch.no_grad():
+        assert ctx.applied == {"matmul": 2, "layernorm": 1, "rmsnorm": 1}
+        assert isinstance(m[0], verify.ModuleLinearWrapper) and isinstance(m[1], verify.ModuleLayerNormWrapper)
+        assert isinstance(m[3], verify.ModuleRMSNormWrapper)
+        out = m(x)
+        calls = ctx.external["layernorm"].module_fn.__globals__["CALLS"]
+        assert calls == [(15, 32)]  # called on the [rows, cols] view
+    torch.testing.assert_close(out, ref, atol=1e-5, rtol=1e-5)
+    assert {n: type(m) for n, m in model.named_modules()} == before
+
+
+def test_external_module_notes_and_precedence(tmp_path):
+    """Unsupported external types are noted and skipped; an external matmul wins over the
+    libak355 matmul strategy; a module without kernel_fn is noted at load."""
+    mm = _write(tmp_path, "kernel_matmul_1_optimized.py", FAKE_MM)
+    bad = _write(tmp_path, "kernel_layernorm_1_optimized.py", "KERNEL_TYPE = 'layernorm'\n")
+    sm = verify.KernelReplacement("softmax", 1, 2.0, mm)
+    m = tiny()
+    ctx = verify.OptimizedModelContext(m, ["matmul", "rmsnorm", verify.replacement_from_module(mm), sm,
+                                           verify.KernelReplacement("layernorm", 1, 0.0, bad)])
+    with ctx:
+        assert ctx.applied["matmul"] == 2 * 7 + 1 and ctx.applied["rmsnorm"] == 5
+        assert all(isinstance(w, verify.ModuleLinearWrapper) for n, w in m.named_modules() if n == "output")
+    assert any("softmax" in n for n in ctx.notes)
+    assert any("no kernel_fn" in n for n in ctx.notes)
+
+
+def test_gpt2_and_bert_strategies_apply_and_restore():
+    """The reference's GPT-2 and BERT architectures (small instances, CPU, no forward): the
+    attention strategies, every remaining Linear and every LayerNorm are swapped and restored."""
+    from autokernel_amd import bert, gpt2
+    for model, attn in ((gpt2.GPT2(vocab_size=64, block_size=32, n_layer=2, n_head=2, n_embd=64),
+                         verify.FusedQKVAttentionWrapper),
+                        (bert.BertModel(vocab_size=64, hidden_size=64, num_layers=2, num_heads=2,
+                                        intermediate_size=128, max_seq_len=32), verify.EncoderAttentionWrapper)):
+        before = {n: type(x) for n, x in model.named_modules()}
+        ctx = verify.OptimizedModelContext(model, verify.ALL_KERNELS)
+        with ctx as m:
+            assert ctx.applied == {"attention": 2, "matmul": 5, "layernorm": 5}, (type(model), ctx.applied)
+            assert sum(isinstance(x, attn) for x in m.modules()) == 2
+        assert {n: type(x) for n, x in model.named_modules()} == before
