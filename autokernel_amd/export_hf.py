@@ -14,7 +14,8 @@ and its C ABI, so the project holds:
     <name>/torch-ext/torch_binding.cpp   one torch op per C entry point (TORCH_LIBRARY_EXPAND)
     <name>/torch-ext/torch_binding.h
     <name>/torch-ext/<name>/__init__.py  kernel_fn of the chosen op type (or every op), KERNEL_TYPE
-    <name>/torch-ext/<name>/_host.py     the reference kernel_fn semantics over the torch ops
+    <name>/torch-ext/<name>/_host.py     the reference kernel_fn semantics over the torch ops: the
+                                         in-tree autokernel_amd/kernels/host.py, copied unchanged
 
 The op type comes from --op, else from the KERNEL_TYPE line of the kernel file (the reference's
 detect_kernel_type, export_hf.py:87-92); "all" exports every op as a named function.
@@ -38,6 +39,8 @@ PKG_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PKG_DIR.parent
 TEMPLATE_DIR = PKG_DIR / "hf_export"
 HEADER = REPO_ROOT / "include" / "ak355.h"
+# the kernel_fn shape / dtype layer, shared with the in-tree package and shipped unchanged
+HOST_LAYER = PKG_DIR / "kernels" / "host.py"
 DEFAULT_KERNEL_PATH = REPO_ROOT / "kernel.py"
 DEFAULT_OUTPUT_DIR = REPO_ROOT / "workspace" / "hf_export"
 ROCM_ARCHS = (_build.ARCH,)
@@ -212,7 +215,7 @@ def export_kernel(name: str, output_dir: str | Path = DEFAULT_OUTPUT_DIR, repo_i
     src.insert(0, f"include/{HEADER.name}")
     for f in ("torch_binding.cpp", "torch_binding.h"):
         shutil.copyfile(TEMPLATE_DIR / f, ext_dir / f)
-    shutil.copyfile(TEMPLATE_DIR / "host.py", mod_dir / "_host.py")
+    shutil.copyfile(HOST_LAYER, mod_dir / "_host.py")
     files = {
         project / "build.toml": generate_build_toml(name, repo_id, src),
         project / "flake.nix": generate_flake_nix(name),

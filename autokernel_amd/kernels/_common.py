@@ -1,4 +1,4 @@
-"""Helpers shared by the kernel_fn modules: device guard and row flattening."""
+"""Helpers shared by the kernel_fn modules: device guard, GPU check and row flattening."""
 from __future__ import annotations
 
 import contextlib
@@ -27,3 +27,11 @@ def match_dtype(t: torch.Tensor | None, dtype: torch.dtype) -> torch.Tensor | No
     if t is None or t.dtype == dtype:
         return t
     return t.to(dtype)
+
+
+def require_gpu(op: str, *tensors: torch.Tensor | None) -> None:
+    """RuntimeError for a CPU tensor: the library has no CPU path."""
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(f"{op}: expected GPU tensors, got a tensor on {t.device} "
+                               "(autokernel_amd has no CPU path)")

@@ -9,13 +9,15 @@ the MFMA kernels, and so do f16 / bf16 heads narrower than 128 (16, 32, 96, ...)
 64 or 128: zero columns add nothing to Q K^T, the padded output columns are dropped, and the scale
 stays D**-0.5 of the true D. fp32, and f16 / bf16 heads wider than 128, run the general kernel, which
 keeps the reference's roundings step by step. Runs ak_flash_attn_fwd (attention.hip).
+kernel_fn is kernels/host.py's flash_attention; attention() is the 4-D form the model plug-in
+uses, which can also write into a strided output view.
 """
 from __future__ import annotations
 
 import torch
 
-from .. import _lib
-from ._common import device_guard
+from . import _ops
+from .host import flash_attention as kernel_fn  # noqa: F401
 
 KERNEL_TYPE = "flash_attention"
 
@@ -41,7 +43,6 @@ def attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, causal: bool = 
         raise ValueError(f"flash_attention: dtype {Q.dtype} unsupported (float16, bfloat16, float32)")
     if not 1 <= D <= 256:
         raise ValueError(f"flash_attention: head_dim {D} unsupported (1 .. 256)")
-    code = _lib.dtype_code(Q, "flash_attention")
     if sm_scale is None:
         sm_scale = D ** -0.5
     if Q.dtype != torch.float32 and D < 128 and D != 64:
@@ -56,24 +57,5 @@ def attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, causal: bool = 
     O = out if out is not None else torch.empty((B, Hq, Sq, D), device=Q.device, dtype=Q.dtype)
     if Sk == 0:
         raise ValueError("flash_attention: empty key sequence")
-    a = [_lib.i64_array(t.stride()[:3]) for t in (Q, K, V, O)]
-    with device_guard(Q):
-        st = _lib.load().ak_flash_attn_fwd(code, Q.data_ptr(), K.data_ptr(), V.data_ptr(),
-                                           O.data_ptr(), B, Hq, Hkv, Sq, Sk, D, a[0], a[1], a[2],
-                                           a[3], int(bool(causal)), float(sm_scale),
-                                           _lib.stream_of(Q))
-    _lib.check(st, "ak_flash_attn_fwd", Q=tuple(Q.shape), K=tuple(K.shape), dtype=Q.dtype)
+    _ops.flash_attn_fwd(O, Q, K, V, bool(causal), float(sm_scale))
     return O
-
-
-def kernel_fn(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, causal: bool = True,
-              sm_scale: float | None = None) -> torch.Tensor:
-    _lib.require_gpu("flash_attention", Q, K, V)
-    if Q.dim() == 3:
-        return attention(Q[None], K[None], V[None], causal, sm_scale)[0]
-    if Q.dim() != 4:
-        raise ValueError(f"flash_attention: expected 3-D or 4-D Q, got {Q.dim()}-D")
-    if K.shape[0] != Q.shape[0] and K.shape[0] == 1:
-        K = K.expand(Q.shape[0], *K.shape[1:])
-        V = V.expand(Q.shape[0], *V.shape[1:])
-    return attention(Q, K, V, causal, sm_scale)

@@ -1,10 +1,13 @@
-"""Python layer of the HuggingFace Kernels ROCm package (shipped as ``_host.py``).
+"""The shape / dtype layer of every kernel_fn: the reference's signatures and semantics
+(reference.py:10-78, kernels/<op>.py kernel_fn) over a namespace of tensor-level ops, one per
+libak355 C entry point (outputs first). Each function checks devices, shapes and dtypes
+(ValueError for a bad argument, RuntimeError for a CPU tensor: there is no CPU path), flattens
+to the rows layout the op takes, allocates the output and calls the op.
 
-The reference's kernel_fn signatures and semantics (reference.py:10-78, kernels/<op>.py kernel_fn)
-over the package's torch ops (torch_binding.cpp), which map one to one onto libak355's C entry
-points: each function checks shapes and dtypes (ValueError), flattens to the rows layout the op
-takes, allocates the output and calls the op. ``bind(ops)`` receives the op namespace (the
-package's ``_ops.ops``) once, at import.
+One layer, two backends: ``bind(ops)`` receives the op namespace once. In-tree it is
+autokernel_amd.kernels._ops (ctypes over libak355.so); the HuggingFace Kernels package ships this
+file unchanged as ``_host.py`` and binds it to its registered torch ops (torch_binding.cpp), which
+have the same names and signatures.
 """
 from __future__ import annotations
 
