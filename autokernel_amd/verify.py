@@ -314,12 +314,28 @@ class AttentionWrapper(nn.Module):
         self.use_rope, self.use_fa, self.use_matmul = use_rope, use_fa, use_matmul
         o = original
         self.n_heads, self.n_kv_heads, self.head_dim = o.n_heads, o.n_kv_heads, o.head_dim
-        # One [H*D + 2*Hk*D, dim] weight for the three projections (copied once, inference only):
-        # one GEMM instead of three, and q / k / v are column slices of its output.
-        self.w_qkv = None
-        if use_matmul and all(getattr(o, n).bias is None for n in ("wq", "wk", "wv")):
+        # One [H*D + 2*Hk*D, dim] weight for the three projections: one GEMM instead of three, and
+        # q / k / v are column slices of its output. It is a copy, rebuilt whenever a source weight
+        # changes (in-place update, optimizer step, load_state_dict: tracked by version and storage).
+        self.fused_qkv = use_matmul and all(getattr(o, n).bias is None for n in ("wq", "wk", "wv"))
+        self._qkv_key = None
+        self._w_qkv = None
+
+    def _qkv_weight(self) -> Optional[torch.Tensor]:
+        if not self.fused_qkv:
+            return None
+        o = self.original
+        ws = (o.wq.weight, o.wk.weight, o.wv.weight)
+        key = tuple((w.data_ptr(), w._version, w.dtype, tuple(w.shape)) for w in ws)
+        if key != self._qkv_key:
             with torch.no_grad():
-                self.w_qkv = torch.cat([o.wq.weight, o.wk.weight, o.wv.weight], 0).contiguous()
+                self._w_qkv = torch.cat(ws, 0).contiguous()
+            self._qkv_key = key
+        return self._w_qkv
+
+    @property
+    def w_qkv(self) -> Optional[torch.Tensor]:
+        return self._qkv_weight()
 
     def _proj(self, lin: nn.Linear, x):
         return _linear(x, lin.weight, lin.bias) if self.use_matmul else lin(x)
@@ -339,14 +355,15 @@ class AttentionWrapper(nn.Module):
         H, Hk, D = self.n_heads, self.n_kv_heads, self.head_dim
         cos, sin = _rope_tables_from(rope_args)
         rotated = False
-        if self.w_qkv is not None:
+        w_qkv = self._qkv_weight()
+        if w_qkv is not None:
             if self.use_rope and x.dtype in (torch.float16, torch.bfloat16) and D % 4 == 0:
                 # q and k heads rotated in the projection's epilogue: no RoPE launch of their own
                 c32, s32 = self._fp32_tables(cos, sin, T)
-                qkv = gemm_rope(x.reshape(B * T, -1), self.w_qkv.t(), c32, s32, T, D, (H + Hk) * D)
+                qkv = gemm_rope(x.reshape(B * T, -1), w_qkv.t(), c32, s32, T, D, (H + Hk) * D)
                 rotated = True
             else:
-                qkv = gemm(x.reshape(B * T, -1), self.w_qkv.t())
+                qkv = gemm(x.reshape(B * T, -1), w_qkv.t())
             q = qkv[:, : H * D].view(B, T, H, D)
             k = qkv[:, H * D: (H + Hk) * D].view(B, T, Hk, D)
             v = qkv[:, (H + Hk) * D:].view(B, T, Hk, D)
@@ -356,7 +373,7 @@ class AttentionWrapper(nn.Module):
             v = self._proj(o.wv, x).view(B, T, Hk, D)
         if self.use_rope and not rotated:
             c32, s32 = self._fp32_tables(cos, sin, T)
-            if self.w_qkv is not None:
+            if w_qkv is not None:
                 # q and k heads are adjacent in each token's row of the fused output: one launch
                 # rotates all H + Hk of them (the same per-element arithmetic as two calls)
                 qk = rope_mod.apply_fp32_tables(qkv[:, : (H + Hk) * D].view(B, T, H + Hk, D), c32, s32)

@@ -248,3 +248,21 @@ def test_gpt2_and_bert_strategies_apply_and_restore():
             assert ctx.applied == {"attention": 2, "matmul": 5, "layernorm": 5}, (type(model), ctx.applied)
             assert sum(isinstance(x, attn) for x in m.modules()) == 2
         assert {n: type(x) for n, x in model.named_modules()} == before
+
+
+def test_fused_qkv_weight_follows_weight_updates():
+    """The fused [wq; wk; wv] copy is rebuilt when a source weight changes in place or is replaced."""
+    import torch
+    m = tiny()
+    with verify.OptimizedModelContext(m, verify.ALL_KERNELS) as pm:
+        wrap = pm.layers[0].original.attention
+        att = wrap.original
+        w0 = wrap.w_qkv
+        assert torch.equal(w0, torch.cat([att.wq.weight, att.wk.weight, att.wv.weight]))
+        assert wrap.w_qkv is w0                      # unchanged weights: no rebuild
+        with torch.no_grad():
+            att.wk.weight.add_(1.0)                  # in-place update
+        w1 = wrap.w_qkv
+        assert w1 is not w0 and torch.equal(w1[att.wq.weight.shape[0]:][:att.wk.weight.shape[0]], att.wk.weight)
+        att.wv.weight = torch.nn.Parameter(torch.zeros_like(att.wv.weight))   # replaced
+        assert torch.count_nonzero(wrap.w_qkv[-att.wv.weight.shape[0]:]) == 0
