@@ -304,8 +304,9 @@ __global__ __launch_bounds__(kFaThreads, 8 / kFaWaves) void fa_fwd(
 //     lane j of a group addresses V[key0 + j / 4][d0 + 4 (j % 4)] and output lane i receives
 //     V[key0 + e][d0 + i], e = 0..3: four consecutive keys of one d, as the MFMA's A operand needs.
 //   * Software pipeline per wave, one tile per iteration j:
-//       phase 1: O^T += V_{j-1}^T P_{j-1}^T (MFMA)   with   row max of S_j (VALU)
-//       phase 2: S_{j+1} = K_{j+1} Q^T (MFMA)        with   P_j = exp2(S_j - m), row sums (VALU)
+//       phase 1: O^T <- alpha_{j-1} O^T + V_{j-1}^T P_{j-1}^T (MFMA; the rescale of each 32-row
+//                block right before its MFMAs)   with   row max of S_j, exponent arguments (VALU)
+//       phase 2: S_{j+1} = K_{j+1} Q^T (MFMA)   with   P_j = exp2(...), packing, row sums (VALU)
 //     so every MFMA burst has independent softmax work beside it. Two barriers per tile (after
 //     each phase); each tile's DMA is issued 1.5 iterations before it is read.
 //   * Scores stay in raw units (Q K^T); the scale is folded into the exp2 argument. The
@@ -314,8 +315,8 @@ __global__ __launch_bounds__(kFaThreads, 8 / kFaWaves) void fa_fwd(
 //     score is at or below minus the threshold (a row of -inf); both are decided once per row from
 //     the true row max.
 //   * Rounding as stock SDPA does it: the exp2 base is the exact running max, so P <= 1 is rounded
-//     to f16 / bf16 for the P V product; row sums add the unrounded fp32 P; O is divided by the
-//     row sum at the end. (A lazily raised base rounds P at other points; measured against SDPA,
+//     to f16 / bf16 for the P V product; row sums add the unrounded fp32 P; O is scaled by the
+//     reciprocal of the row sum at the end. (A lazily raised base rounds P at other points; measured against SDPA,
 //     this arithmetic agrees bit for bit on 97 % of outputs, the lazy base on 59 %.)
 // LDS swizzles (16-byte chunk c of row r):
 //   K: c ^ (r & 15) for D = 128, c ^ ((r >> 1) & 7) for D = 64. gfx950 serves a ds_read_b128 in
@@ -504,11 +505,15 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   const int vcol = 16 * (g16 & 1) + 4 * (i16 & 3);       // + 32 db
   const int vsw = fa2_vswz<D>(vrow);                      // same for rows + 8, + 16 t
   u32x4 pf[4];
-  auto pv = [&](const uint16_t* vs) {
+  // O^T <- alpha O^T + V^T P^T, one 32-row d block at a time: each block is rescaled right before its
+  // four MFMAs, so the multiplies of block db + 1 run beside the MFMAs of block db.
+  auto pv = [&](const uint16_t* vs, float alpha) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int db = 0; db < NDB; ++db) {
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
+      for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
         const int col = db * 32 + vcol;
         const uint16_t* p = vs + (16 * t + vrow) * D + (((col >> 3) ^ vsw) * 8) + (col & 7);
         const u32x2 lo = fa2_tr16(p);
@@ -516,9 +521,13 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
         const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
         o[db] = mfma32x32x16<T>(vf, pf[t], o[db]);
       }
+    }
   };
 
   float m_run = -INFINITY, l_run = 0.f, m_true = -INFINITY;
+  // rescale factor of the last tile whose P V product is still to be added: O is brought to that
+  // tile's exp2 base right before the product (deferred from the tile's own statistics)
+  float alpha_pend = 1.0f;
   // row statistics of S_j: mask, tile max (raw units), lazy base update
   auto stats = [&](f32x16 (&s)[2], int k0, bool masked, float& alpha, float& base) {
     if (masked) {
@@ -589,14 +598,16 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
     else if (later == 1) dma_barrier<NIW>();
     else dma_barrier<0>();
   };
+  // At j = 0 the prologue has already waited for K_0, K_1 and V_0; only K_2 (issued after that
+  // wait) and V_1 (mid 0) can be in flight, and neither is needed before iteration 1.
   auto sync_mid = [&](int j, int par) {
-    // issued after K_{j+1}: V_j (mid j-1; in the prologue for j = 0, waited there) and K_{j+2}
-    barrier_after(j == 0 ? 0 : 1 + (j + 2 < nt));
+    // issued after K_{j+1}: V_j (mid j-1) and K_{j+2}
+    barrier_after(j == 0 ? (nt > 2) : 1 + (j + 2 < nt));
     if (j + 1 < nt) issue_v(j + 1, par ^ 1);
   };
   auto sync_end = [&](int j, int par) {
-    // issued after V_j: K_{j+2} (end j-1) and V_{j+1} (mid j); V_0 was waited in the prologue
-    barrier_after(j == 0 ? 0 : (j + 2 < nt) + (j + 1 < nt));
+    // issued after V_j: K_{j+2} (end j-1) and V_{j+1} (mid j)
+    barrier_after((j + 2 < nt) + (j + 1 < nt));
     if (j + 3 < nt) issue_k(j + 3, par ^ 1);
   };
   f32x16 sa[2], sb[2];
@@ -605,7 +616,7 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   // masked.
   auto iter = [&](int j, int par, f32x16 (&S)[2], f32x16 (&Sn)[2]) {
     const int k0 = j * kFaBKV;
-    if (j > 0 && j - 1 <= jw) pv(sV + (par ^ 1) * TILE);  // V_{j-1}
+    if (j > 0 && j - 1 <= jw) pv(sV + (par ^ 1) * TILE, alpha_pend);  // V_{j-1}
     float alpha = 1.0f, base = 0.f;
     const bool act = j <= jw;
     if (act) {
@@ -618,35 +629,34 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
       exp_args(S, base);
       const float ps = exp_pack(S);
       l_run = l_run * alpha + ps;
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
-#pragma unroll
-        for (int i = 0; i < NDB; ++i)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) o[i][v] *= alpha;
-      }
+      alpha_pend = alpha;
     }
     sync_end(j, par);
   };
   // Steady-state iteration (1 <= j, tile j unmasked, j + 1 <= jw): all four parts run, with no
   // branch between them, so the MFMAs of one part and the VALU work of the other share one block.
   auto iter_fast = [&](int j, int par, f32x16 (&S)[2], f32x16 (&Sn)[2]) {
-    // phase 1: O^T += V_{j-1}^T P_{j-1}^T beside the row max of S_j and its exponent arguments.
-    // Fragment reads run two MFMAs ahead of their use.
-    pv(sV + (par ^ 1) * TILE);
+    // phase 1: O^T <- alpha_{j-1} O^T + V_{j-1}^T P_{j-1}^T beside the row max of S_j and its
+    // exponent arguments (pinned here, so that phase 2 holds only the exponentials, the packing and
+    // the row sums). Fragment reads run two MFMAs ahead of their use. The rescale is unconditional:
+    // a branch around it duplicates the block and costs more in register moves than it saves.
+    pv(sV + (par ^ 1) * TILE, alpha_pend);
     float alpha, base;
     stats(S, j * kFaBKV, false, alpha, base);
     exp_args(S, base);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) asm volatile("" ::"v"(S[kb]));
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
     for (int i = 0; i < 14; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the V^T fragment of MFMA i + 2
-      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // 5 VALU
+      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // 8 VALU
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     sync_mid(j, par);
@@ -662,21 +672,16 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
     for (int i = 0; i < 14; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // 1 MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);  // the K fragment of MFMA i + 2
-      __builtin_amdgcn_sched_group_barrier(0x402, 4, 1);  // 4 VALU / transcendental
+      __builtin_amdgcn_sched_group_barrier(0x402, 5, 1);  // 5 VALU / transcendental
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x402, 4, 1);
+      __builtin_amdgcn_sched_group_barrier(0x402, 5, 1);
     }
     __builtin_amdgcn_sched_barrier(0);
     l_run = l_run * alpha + ps;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
-#pragma unroll
-      for (int i = 0; i < NDB; ++i)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[i][v] *= alpha;
-    }
+    alpha_pend = alpha;
     sync_end(j, par);
   };
 
@@ -711,13 +716,13 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) sa[kb] = sb[kb];
   }
-  if (nt - 1 <= jw) pv(sV + ((nt - 1) & 1) * TILE);
+  if (nt - 1 <= jw) pv(sV + ((nt - 1) & 1) * TILE, alpha_pend);
   wait_vmcnt<0>();  // (no transfer is outstanding here; kept so none can outlive the block)
 
   // ---- epilogue: O[q][d] = O^T[d][q] / l; NaN rows where the reference's scores overflow ----
-  // a NaN row divides by NaN
+  // one correctly rounded reciprocal per row, then products (a NaN row multiplies by NaN)
   const bool nan_row = !(m_true < thr && m_true > -thr);
-  const float l_tot = nan_row ? __builtin_nanf("") : fa2_halves_sum(l_run);
+  const float inv = nan_row ? __builtin_nanf("") : 1.0f / fa2_halves_sum(l_run);
   if (my_q < Sq) {
     uint16_t* orow = Ob + (int64_t)my_q * oss;
 #pragma unroll
@@ -726,8 +731,8 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
       for (int g = 0; g < 4; ++g) {
         const int d = db * 32 + g * 8 + hh * 4;
         u32x2 pk;
-        pk[0] = fa2_pack<T>(o[db][g * 4 + 0] / l_tot, o[db][g * 4 + 1] / l_tot);
-        pk[1] = fa2_pack<T>(o[db][g * 4 + 2] / l_tot, o[db][g * 4 + 3] / l_tot);
+        pk[0] = fa2_pack<T>(o[db][g * 4 + 0] * inv, o[db][g * 4 + 1] * inv);
+        pk[1] = fa2_pack<T>(o[db][g * 4 + 2] * inv, o[db][g * 4 + 3] * inv);
         *reinterpret_cast<u32x2*>(orow + d) = pk;
       }
   }
