@@ -85,9 +85,11 @@ struct TBF16 {
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
-// Nontemporal store: data written once and not read back soon.
+// Nontemporal store: data written once and not read back soon. Written as the instruction itself:
+// a branch between this and a plain store (a run-time choice) would otherwise be merged into one
+// plain store by the compiler, which drops the nontemporal hint.
 __device__ __forceinline__ void st16_stream(void* p, const u32x4& v) {
-  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+  asm volatile("global_store_dwordx4 %0, %1, off nt" ::"v"(p), "v"(v) : "memory");
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -100,6 +100,13 @@ def run_mfma() -> None:
     from . import kernels, spec
     dev = torch.device("cuda:0")
     flush = torch.empty(512 * 2 ** 20, dtype=torch.uint8, device=dev)
+    # the calibration copy of `run` (FETCH_SIZE / WRITE_SIZE scale), before the matrix kernels
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        flush.zero_()
+        dst.copy_(src)
+    del src, dst
     m = spec.baseline_matmul(device=dev)
     g = torch.Generator(device=dev).manual_seed(0)
     a8 = (torch.randn(8192, 8192, device=dev, generator=g) / 8192 ** 0.5).bfloat16()
@@ -192,6 +199,59 @@ def summarize_mfma(dirpath: str) -> None:
     print("\n".join(lines))
 
 
+# unique bytes each matrix workload must move at least once (inputs read, output written)
+MFMA_IDEAL_BYTES = {
+    "matmul4k": 3 * 4096 * 4096 * 2,
+    "matmul8k": 3 * 8192 * 8192 * 2,
+    "mlp_gateup": (2048 * 4096 + 2 * 11008 * 4096 + 2048 * 11008) * 2,
+    "mlp_down": (2048 * 11008 + 4096 * 11008 + 2048 * 4096) * 2,
+    "fa2k": 4 * 4 * 32 * 2048 * 128 * 2,
+    "fa8k": 4 * 32 * 8192 * 128 * 2,
+}
+
+
+def summarize_mfma_traffic(dirpath: str) -> None:
+    """Traffic past L2 (FETCH_SIZE / WRITE_SIZE, calibrated on the copy) and the L2 hit rate of each
+    matrix kernel against the unique bytes its workload must move, per GFLOP."""
+    passes = _dispatches(dirpath)
+    allrows = [x for disp in passes for x in disp]
+    cal = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        vals = [c[ctr] for _, n, c, _ in allrows if ctr in c and ("copy" in n.lower() or "elementwise" in n.lower())
+                and c[ctr] * 1024 > COPY_BYTES / 4]
+        cal[ctr] = COPY_BYTES / (1024 * sum(vals) / len(vals)) if vals else 1.0
+    keys = ["matmul4k", "matmul8k", "mlp_gateup", "mlp_down", "fa2k", "fa8k"]
+    lines = ["# Traffic past L2 of the matrix kernels (rocprofv3 PMC)", "",
+             "Commands (one counter group per run):", "",
+             "    rocprofv3 --pmc FETCH_SIZE -d DIR -o fetch --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma",
+             "    rocprofv3 --pmc WRITE_SIZE -d DIR -o write --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma",
+             "    rocprofv3 --pmc TCC_HIT_sum TCC_MISS_sum -d DIR -o l2 --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma",
+             "    python -m autokernel_amd.roofline_probe summarize_mfma_traffic DIR", "",
+             f"FETCH / WRITE_SIZE count bytes leaving the L2s for the fabric (Infinity Cache or HBM), scaled by a "
+             f"{COPY_BYTES >> 20} MiB copy: FETCH x{cal['FETCH_SIZE']:.3f}, WRITE x{cal['WRITE_SIZE']:.3f}. Unique = the "
+             "bytes the workload must move at least once. Three launches each, caches flushed before every launch.", "",
+             "| kernel | workload | GFLOP | unique MB | fetched MB | written MB | fetched / unique | bytes past L2 per FLOP | L2 hit rate |",
+             "|---|---|---|---|---|---|---|---|---|"]
+    for pi, (frag, label, flops, _) in enumerate(MFMA_PROBES):
+        k = sum(1 for q in MFMA_PROBES[:pi] if q[0] == frag)
+        ctr = defaultdict(list)
+        for disp in passes:
+            same = [x for x in disp if frag in x[1]]
+            for _, name, c, _d in same[3 * k:3 * k + 3]:
+                for n, v in c.items():
+                    ctr[n].append(v)
+        if not ctr:
+            continue
+        c = {n: sum(v) / len(v) for n, v in ctr.items()}
+        fetch = c.get("FETCH_SIZE", float("nan")) * 1024 * cal["FETCH_SIZE"]
+        write = c.get("WRITE_SIZE", float("nan")) * 1024 * cal["WRITE_SIZE"]
+        hit = c.get("TCC_HIT_sum", float("nan")) / max(c.get("TCC_HIT_sum", 0.0) + c.get("TCC_MISS_sum", 0.0), 1.0)
+        uniq = MFMA_IDEAL_BYTES[keys[pi]]
+        lines.append(f"| {frag.split('(')[0]} | {label} | {flops / 1e9:.1f} | {uniq / 1e6:.1f} | {fetch / 1e6:.1f} | "
+                     f"{write / 1e6:.1f} | {fetch / uniq:.2f} | {(fetch + write) / flops:.4f} | {100 * hit:.1f}% |")
+    print("\n".join(lines))
+
+
 def _read(dirpath: str):
     """{kernel name: {counter: [values per dispatch]}} from rocprofv3 counter_collection CSVs."""
     out = defaultdict(lambda: defaultdict(list))
@@ -243,6 +303,8 @@ if __name__ == "__main__":
         summarize(sys.argv[2])
     elif cmd == "summarize_mfma":
         summarize_mfma(sys.argv[2])
+    elif cmd == "summarize_mfma_traffic":
+        summarize_mfma_traffic(sys.argv[2])
     elif cmd == "run_mfma":
         run_mfma()
     else:
