@@ -304,9 +304,9 @@ __global__ __launch_bounds__(kFaThreads, 8 / kFaWaves) void fa_fwd(
 //     lane j of a group addresses V[key0 + j / 4][d0 + 4 (j % 4)] and output lane i receives
 //     V[key0 + e][d0 + i], e = 0..3: four consecutive keys of one d, as the MFMA's A operand needs.
 //   * Software pipeline per wave, one tile per iteration j:
-//       phase 1: O^T <- alpha_{j-1} O^T + V_{j-1}^T P_{j-1}^T (MFMA; the rescale of each 32-row
-//                block right before its MFMAs)   with   row max of S_j, exponent arguments (VALU)
-//       phase 2: S_{j+1} = K_{j+1} Q^T (MFMA)   with   P_j = exp2(...), packing, row sums (VALU)
+//       phase 1: O^T += V_{j-1}^T P_{j-1}^T (MFMA)   with   row max of S_j, exponent arguments (VALU)
+//       phase 2: S_{j+1} = K_{j+1} Q^T (MFMA)        with   P_j = exp2(...), packing, row sums and the
+//                                                           rescale O^T <- alpha_j O^T (VALU)
 //     so every MFMA burst has independent softmax work beside it. Two barriers per tile (after
 //     each phase); each tile's DMA is issued 1.5 iterations before it is read.
 //   * Scores stay in raw units (Q K^T); the scale is folded into the exp2 argument. The
@@ -379,6 +379,8 @@ __device__ __forceinline__ uint32_t fa2_pack<TBF16>(float a, float b) {
   typedef __bf16 b2 __attribute__((ext_vector_type(2)));
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, b2));
 }
+// Keeps the computation of x ahead of this point (an empty use the compiler cannot move).
+__device__ __forceinline__ void fa2_pin(const f32x16& x) { asm volatile("" ::"v"(x)); }
 // max over the two 32-lane halves (every lane gets the same value, combined in the same order)
 __device__ __forceinline__ float fa2_halves_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -505,13 +507,11 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   const int vcol = 16 * (g16 & 1) + 4 * (i16 & 3);       // + 32 db
   const int vsw = fa2_vswz<D>(vrow);                      // same for rows + 8, + 16 t
   u32x4 pf[4];
-  // O^T <- alpha O^T + V^T P^T, one 32-row d block at a time: each block is rescaled right before its
-  // four MFMAs, so the multiplies of block db + 1 run beside the MFMAs of block db.
-  auto pv = [&](const uint16_t* vs, float alpha) {
+  // O^T += V^T P^T over the 64 keys of a tile, one 32-row d block at a time (O^T already carries the
+  // tile's exp2 base: it was rescaled in the previous phase).
+  auto pv = [&](const uint16_t* vs) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int col = db * 32 + vcol;
@@ -525,9 +525,6 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   };
 
   float m_run = -INFINITY, l_run = 0.f, m_true = -INFINITY;
-  // rescale factor of the last tile whose P V product is still to be added: O is brought to that
-  // tile's exp2 base right before the product (deferred from the tile's own statistics)
-  float alpha_pend = 1.0f;
   // row statistics of S_j: mask, tile max (raw units), lazy base update
   auto stats = [&](f32x16 (&s)[2], int k0, bool masked, float& alpha, float& base) {
     if (masked) {
@@ -616,7 +613,7 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   // masked.
   auto iter = [&](int j, int par, f32x16 (&S)[2], f32x16 (&Sn)[2]) {
     const int k0 = j * kFaBKV;
-    if (j > 0 && j - 1 <= jw) pv(sV + (par ^ 1) * TILE, alpha_pend);  // V_{j-1}
+    if (j > 0 && j - 1 <= jw) pv(sV + (par ^ 1) * TILE);  // V_{j-1}
     float alpha = 1.0f, base = 0.f;
     const bool act = j <= jw;
     if (act) {
@@ -629,18 +626,21 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
       exp_args(S, base);
       const float ps = exp_pack(S);
       l_run = l_run * alpha + ps;
-      alpha_pend = alpha;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
     }
     sync_end(j, par);
   };
   // Steady-state iteration (1 <= j, tile j unmasked, j + 1 <= jw): all four parts run, with no
   // branch between them, so the MFMAs of one part and the VALU work of the other share one block.
   auto iter_fast = [&](int j, int par, f32x16 (&S)[2], f32x16 (&Sn)[2]) {
-    // phase 1: O^T <- alpha_{j-1} O^T + V_{j-1}^T P_{j-1}^T beside the row max of S_j and its
-    // exponent arguments (pinned here, so that phase 2 holds only the exponentials, the packing and
-    // the row sums). Fragment reads run two MFMAs ahead of their use. The rescale is unconditional:
-    // a branch around it duplicates the block and costs more in register moves than it saves.
-    pv(sV + (par ^ 1) * TILE, alpha_pend);
+    // phase 1: O^T += V_{j-1}^T P_{j-1}^T beside the row max of S_j and its exponent arguments
+    // (pinned here, so that phase 2 holds only the exponentials, the packing, the row sums and the
+    // rescale). Nothing in this phase waits on VALU results, so one MFMA, two fragment reads and five
+    // VALU instructions interleave throughout; fragment reads run one MFMA ahead of their use.
+    pv(sV + (par ^ 1) * TILE);
     float alpha, base;
     stats(S, j * kFaBKV, false, alpha, base);
     exp_args(S, base);
@@ -651,37 +651,45 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
     for (int i = 0; i < 14; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the V^T fragment of MFMA i + 2
-      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // 8 VALU
+      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // 5 VALU
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     sync_mid(j, par);
-    // phase 2: S_{j+1} = K_{j+1} Q^T beside P_j = exp2(...) and its row sum
+    // phase 2: S_{j+1} = K_{j+1} Q^T beside P_j = exp2(...), its row sum and O^T <- alpha_j O^T
+    // (O^T is not touched by this phase's MFMAs). The rescale is unconditional: a branch around it
+    // duplicates the block and costs more in register moves than it saves.
     qk(sK + (par ^ 1) * TILE, Sn);
     const float ps = exp_pack(S);
-    // keep P_j's computation here (otherwise it sinks to its first use after the barrier)
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+    // keep P_j's computation and the rescale here (otherwise they sink to their first use after the
+    // barrier)
 #pragma unroll
     for (int t = 0; t < 4; ++t) asm volatile("" ::"v"(pf[t]));
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) fa2_pin(o[db]);
     asm volatile("" ::"v"(ps));
     __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
 #pragma unroll
     for (int i = 0; i < 14; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // 1 MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);  // the K fragment of MFMA i + 2
-      __builtin_amdgcn_sched_group_barrier(0x402, 5, 1);  // 5 VALU / transcendental
+      __builtin_amdgcn_sched_group_barrier(0x402, 9, 1);  // 9 VALU / transcendental
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x402, 5, 1);
+      __builtin_amdgcn_sched_group_barrier(0x402, 9, 1);
     }
     __builtin_amdgcn_sched_barrier(0);
     l_run = l_run * alpha + ps;
-    alpha_pend = alpha;
     sync_end(j, par);
   };
 
@@ -716,7 +724,7 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) sa[kb] = sb[kb];
   }
-  if (nt - 1 <= jw) pv(sV + ((nt - 1) & 1) * TILE, alpha_pend);
+  if (nt - 1 <= jw) pv(sV + ((nt - 1) & 1) * TILE);
   wait_vmcnt<0>();  // (no transfer is outstanding here; kept so none can outlive the block)
 
   // ---- epilogue: O[q][d] = O^T[d][q] / l; NaN rows where the reference's scores overflow ----

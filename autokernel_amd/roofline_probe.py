@@ -199,6 +199,61 @@ def summarize_mfma(dirpath: str) -> None:
     print("\n".join(lines))
 
 
+STALL_PASSES = (
+    "SQ_VALU_MFMA_BUSY_CYCLES SQ_VALU_MFMA_COEXEC_CYCLES SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_VALU2 SQ_INSTS_VALU "
+    "SQ_INSTS_MFMA SQ_WAVE_CYCLES SQ_BUSY_CYCLES GRBM_GUI_ACTIVE",
+    "SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY SQ_ACTIVE_INST_LDS SQ_LDS_DATA_FIFO_FULL SQ_LDS_CMD_FIFO_FULL "
+    "SQ_INSTS_LDS_LOAD_BANDWIDTH SQ_WAVE_CYCLES GRBM_GUI_ACTIVE",
+)
+
+
+def summarize_mfma_stall(dirpath: str) -> None:
+    """Where the matrix kernels' SIMD cycles go: MFMA busy, VALU issued beside a busy MFMA unit,
+    time waves spend in s_waitcnt / s_barrier or ready but not issued, LDS pressure."""
+    passes = _dispatches(dirpath)
+    lines = ["# Issue and stall counters of the matrix kernels (rocprofv3 PMC)", "",
+             "Commands (two counter passes of eight SQ counters each, then the summary):", ""]
+    lines += [f"    rocprofv3 --pmc {p} -d DIR -o stall_{'ab'[i]} --output-format csv -- "
+              "python -m autokernel_amd.roofline_probe run_mfma" for i, p in enumerate(STALL_PASSES)]
+    lines += ["    python -m autokernel_amd.roofline_probe summarize_mfma_stall DIR", "",
+              "* SIMD-cycles = GRBM_GUI_ACTIVE / 8 XCDs x 256 CUs x 4 SIMDs. MFMA busy and MFMA + VALU co-issue",
+              "  (SQ_VALU_MFMA_COEXEC_CYCLES: a VALU instruction issued while the MFMA unit was busy) are per",
+              "  SIMD-cycle.",
+              "* Wave-time shares are per SQ_WAVE_CYCLES: VALU active (SQ_ACTIVE_INST_VALU), waiting in",
+              "  s_waitcnt / s_barrier (SQ_WAIT_ANY), ready but not issued because the unit or port it needs",
+              "  was taken (SQ_WAIT_INST_ANY; with two waves per SIMD this includes the other wave's MFMAs).",
+              "* LDS command FIFO full: SQ_LDS_CMD_FIFO_FULL per shader engine (32) per kernel cycle.",
+              "* LDS bytes per MFMA: SQ_INSTS_LDS_LOAD_BANDWIDTH x 64 / SQ_INSTS_MFMA (16x16x32 MFMAs in the",
+              "  GEMMs, 32x32x16 in attention, 16 and 32 KFLOP each). Three launches per workload.", "",
+              "| kernel | workload | MFMA busy | MFMA + VALU co-issue | VALU instr. per MFMA | VALU active | "
+              "in s_waitcnt / s_barrier | ready, not issued | LDS cmd FIFO full | LDS bytes per MFMA |",
+              "|---|---|---|---|---|---|---|---|---|---|"]
+    for pi, (frag, label, _flops, _) in enumerate(MFMA_PROBES):
+        k = sum(1 for q in MFMA_PROBES[:pi] if q[0] == frag)
+        ctr = defaultdict(list)
+        for disp in passes:
+            same = [x for x in disp if frag in x[1]]
+            for _, _name, c, _d in same[3 * k:3 * k + 3]:
+                for n, v in c.items():
+                    ctr[n].append(v)
+        if not ctr:
+            continue
+        c = {n: sum(v) / len(v) for n, v in ctr.items()}
+        nan = float("nan")
+        grbm = c.get("GRBM_GUI_ACTIVE", nan) / 8
+        simd = grbm * 256 * 4
+        wc = c.get("SQ_WAVE_CYCLES", nan)
+        mfma = c.get("SQ_INSTS_MFMA", nan)
+        lines.append(
+            f"| {frag.split('(')[0]} | {label} | {100 * c.get('SQ_VALU_MFMA_BUSY_CYCLES', nan) / simd:.1f}% | "
+            f"{100 * c.get('SQ_VALU_MFMA_COEXEC_CYCLES', nan) / simd:.1f}% | "
+            f"{(c.get('SQ_INSTS_VALU', nan) - mfma) / mfma:.1f} | {100 * c.get('SQ_ACTIVE_INST_VALU', nan) / wc:.0f}% | "
+            f"{100 * c.get('SQ_WAIT_ANY', nan) / wc:.0f}% | {100 * c.get('SQ_WAIT_INST_ANY', nan) / wc:.0f}% | "
+            f"{100 * c.get('SQ_LDS_CMD_FIFO_FULL', nan) / 32 / grbm:.1f}% | "
+            f"{64 * c.get('SQ_INSTS_LDS_LOAD_BANDWIDTH', nan) / mfma:.0f} |")
+    print("\n".join(lines))
+
+
 # unique bytes each matrix workload must move at least once (inputs read, output written)
 MFMA_IDEAL_BYTES = {
     "matmul4k": 3 * 4096 * 4096 * 2,
@@ -305,6 +360,8 @@ if __name__ == "__main__":
         summarize_mfma(sys.argv[2])
     elif cmd == "summarize_mfma_traffic":
         summarize_mfma_traffic(sys.argv[2])
+    elif cmd == "summarize_mfma_stall":
+        summarize_mfma_stall(sys.argv[2])
     elif cmd == "run_mfma":
         run_mfma()
     else:
