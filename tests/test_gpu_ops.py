@@ -432,6 +432,12 @@ def test_softmax_ce_wide_odd_rows(gpu, cols, dtype):
     y = sm(x.to(gpu))
     assert_close(y, R.softmax_ref(x), tol, tol, f"softmax wide {cols} {dtype}")
     assert torch.equal(y, sm(x.to(gpu))), "softmax wide rerun differs"
+    # the input one element past an aligned base: its rows no longer share the output's dword
+    # alignment, so 16-bit rows take the unpacked wide kernel
+    buf = torch.empty(x.numel() + 1, dtype=dtype, device=gpu)
+    buf[1:] = x.flatten().to(gpu)
+    y_off = sm(buf[1:].view_as(x))
+    assert_close(y_off, R.softmax_ref(x), tol, tol, f"softmax wide {cols} {dtype}, offset input")
     tg = torch.randint(0, cols, (6,), generator=g)
     tg[1] = 7  # a -inf logit: loss +inf, as the oracle gives
     tg[4] = -100
