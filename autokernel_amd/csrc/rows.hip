@@ -430,6 +430,92 @@ __global__ __launch_bounds__(kWideThreads, 2) void softmax_wide_pairs(const uint
   if (w.has_xt) yr[threadIdx.x == 0 ? 0 : cols - 1] = T::from_f(e(w.xt) * inv);
 }
 
+// Streaming row statistics for 16-bit rows that do not vectorise (softmax_stream, ce_stream): one
+// row per 256-thread block, read once as aligned dword pairs (the WidePairs layout) with an online
+// (max, sum) per thread and 8 pairs in flight per thread. Nothing is cached in registers, so up to
+// eight rows are in flight per CU. Per chunk of 16 elements: the chunk max (NaN-propagating), one
+// rescale of the running sum, then exp2((x - max) log2 e) per element; the per-thread (max, sum)
+// pairs combine in a fixed order (block_combine_ms), as in the looped kernels.
+constexpr int kStreamUnroll = 8;
+template <typename T>
+__device__ __forceinline__ void stream_ms(const uint16_t* xr, int cols, float* red, float* M, float* S) {
+  const int par = (int)(((uintptr_t)xr >> 1) & 1u);
+  const int npairs = (cols - par) >> 1;
+  const __amdgpu_buffer_rsrc_t r = row_rsrc(xr + par, npairs * 4);
+  float m = -INFINITY, s = 0.f;
+  // fold a chunk with maximum cm and values v[0..n) into (m, s)
+  auto fold = [&](float cm, auto&& each) {
+    const float mn = __builtin_elementwise_maximum(m, cm);
+    if (mn == -INFINITY) return;  // nothing but -inf so far
+    s = (m == -INFINITY) ? 0.f : s * fast_exp2((m - mn) * kLog2e);
+    each([&](float v) { s += fast_exp2((v - mn) * kLog2e); });
+    m = mn;
+  };
+  if ((threadIdx.x == 0 && par) || (threadIdx.x == 1 && ((cols - par) & 1))) {
+    const float v = T::to_f(xr[threadIdx.x == 0 ? 0 : cols - 1]);
+    fold(v, [&](auto&& f) { f(v); });
+  }
+  for (int b = 0; b < npairs; b += kLoopThreads * kStreamUnroll) {
+    uint32_t p[kStreamUnroll];
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u)
+      p[u] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)threadIdx.x * 4, (b + u * kLoopThreads) * 4, 0);
+    float cm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u)
+      if (b + u * kLoopThreads + (int)threadIdx.x < npairs)
+        cm = __builtin_elementwise_maximum(cm, __builtin_elementwise_maximum(WidePairs<T, 1>::lo(p[u]), WidePairs<T, 1>::hi(p[u])));
+    fold(cm, [&](auto&& f) {
+#pragma unroll
+      for (int u = 0; u < kStreamUnroll; ++u)
+        if (b + u * kLoopThreads + (int)threadIdx.x < npairs) {
+          f(WidePairs<T, 1>::lo(p[u]));
+          f(WidePairs<T, 1>::hi(p[u]));
+        }
+    });
+  }
+  OnlineMS a;
+  a.m = m;
+  a.s = s;
+  a.nan = (m != m);
+  block_combine_ms(a, red, M, S);
+}
+
+// Streaming softmax for 16-bit rows: the online pass above, then a second read of the row (from
+// the caches when they still hold it) that writes exp2((x - M) log2 e) / S as dword pairs.
+template <typename T>
+__global__ __launch_bounds__(kLoopThreads) void softmax_stream(const uint16_t* __restrict__ x,
+                                                               uint16_t* __restrict__ y, int cols) {
+  __shared__ float red[kLoopThreads / kWave];
+  const int64_t base = (int64_t)blockIdx.x * cols;
+  const uint16_t* xr = x + base;
+  uint16_t* yr = y + base;
+  float M, S;
+  stream_ms<T>(xr, cols, red, &M, &S);
+  const float inv = 1.0f / S;
+  auto e = [&](float v) { return T::from_f(fast_exp2((v - M) * kLog2e) * inv); };
+  const int par = (int)(((uintptr_t)xr >> 1) & 1u);
+  const int npairs = (cols - par) >> 1;
+  const __amdgpu_buffer_rsrc_t r = row_rsrc(xr + par, npairs * 4);
+  const __amdgpu_buffer_rsrc_t w = row_rsrc(yr + par, npairs * 4);
+  if ((threadIdx.x == 0 && par) || (threadIdx.x == 1 && ((cols - par) & 1))) {
+    const int c = threadIdx.x == 0 ? 0 : cols - 1;
+    yr[c] = e(T::to_f(xr[c]));
+  }
+  for (int b = 0; b < npairs; b += kLoopThreads * kStreamUnroll) {
+    uint32_t p[kStreamUnroll];
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u)
+      p[u] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)threadIdx.x * 4, (b + u * kLoopThreads) * 4, 0);
+#pragma unroll
+    for (int u = 0; u < kStreamUnroll; ++u)
+      if (b + u * kLoopThreads + (int)threadIdx.x < npairs) {
+        const uint32_t o = (uint32_t)e(WidePairs<T, 1>::lo(p[u])) | ((uint32_t)e(WidePairs<T, 1>::hi(p[u])) << 16);
+        __builtin_amdgcn_raw_buffer_store_b32(o, w, (int)threadIdx.x * 4, (b + u * kLoopThreads) * 4, 0);
+      }
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kLoopThreads) void softmax_loop(
     const typename T::S* __restrict__ x, typename T::S* __restrict__ y, int cols) {
@@ -468,16 +554,18 @@ static int launch_softmax(const void* x, void* y, int64_t rows, int64_t cols, hi
       launch_timed(softmax_rows<T, L, VPT>, grid, dim3(RowGeom<L>::kThreads), 0, s, xp, yp, rows, (int)cols, nt_out);
     });
   }
-  // 16-bit rows that do not vectorise: the packed wide kernel when x and y rows share their dword
-  // alignment (measured, f16 [4096, 50257]: 234.9 us with the fp32-cached kernel, one row per CU)
+  // 16-bit rows that do not vectorise, when x and y rows share their dword alignment: the streaming
+  // kernel up to 32768 columns and past 65536, the packed register-cached one in between (measured,
+  // f16, 4096 rows: 16385 columns 67.0 us streaming / 99.3 us packed; 24577: 101 / 115; 32769: 138 /
+  // 136; 40961: 182 / 152; 50257: 230 / 180 (the fp32-cached kernel: 234.9)).
   if constexpr (sizeof(S) == 2) {
-    if (!handled && cols > 4096 && cols <= 64 * kWideThreads && ((((uintptr_t)x ^ (uintptr_t)y) & 3u) == 0)) {
+    if (!handled && cols > 4096 && ((((uintptr_t)x ^ (uintptr_t)y) & 3u) == 0)) {
       const uint16_t* xs = (const uint16_t*)x;
       uint16_t* ys = (uint16_t*)y;
-      if (cols <= 16 * kWideThreads)
-        launch_timed(softmax_wide_pairs<T, 8>, dim3((unsigned)rows), dim3(kWideThreads), 0, s, xs, ys, (int)cols);
-      else
+      if (cols > 32768 && cols <= 64 * kWideThreads)
         launch_timed(softmax_wide_pairs<T, 32>, dim3((unsigned)rows), dim3(kWideThreads), 0, s, xs, ys, (int)cols);
+      else
+        launch_timed(softmax_stream<T>, dim3((unsigned)rows), dim3(kLoopThreads), 0, s, xs, ys, (int)cols);
       handled = true;
     }
   }
@@ -568,18 +656,17 @@ __global__ __launch_bounds__(kWideThreads) void ce_wide(const typename T::S* __r
   if (threadIdx.x == 0) loss[blockIdx.x] = ce_row_loss_b2<T>(xr, tgt[blockIdx.x], cols, ignore_index, mb, s);
 }
 
-template <typename T, int NP>
-__global__ __launch_bounds__(kWideThreads, 2) void ce_wide_pairs(const uint16_t* __restrict__ x,
-                                                                const int64_t* __restrict__ tgt,
-                                                                float* __restrict__ loss, int cols,
-                                                                int64_t ignore_index) {
-  __shared__ float red[kWideThreads / kWave];
+// Cross-entropy of a 16-bit row from the streaming statistics: loss = x_t - M - log S, as in ce_loop.
+template <typename T>
+__global__ __launch_bounds__(kLoopThreads) void ce_stream(const uint16_t* __restrict__ x,
+                                                          const int64_t* __restrict__ tgt,
+                                                          float* __restrict__ loss, int cols,
+                                                          int64_t ignore_index) {
+  __shared__ float red[kLoopThreads / kWave];
   const uint16_t* xr = x + (int64_t)blockIdx.x * cols;
-  WidePairs<T, NP> w;
-  const float m = group_reduce<kWideThreads, 1>(w.load_max(xr, cols), red);
-  const float mb = m * kLog2e;
-  const float s = group_reduce<kWideThreads, 0>(w.sum([&](float v) { return fast_exp2(__builtin_fmaf(v, kLog2e, -mb)); }), red);
-  if (threadIdx.x == 0) loss[blockIdx.x] = ce_row_loss_b2<T>(xr, tgt[blockIdx.x], cols, ignore_index, mb, s);
+  float M, S;
+  stream_ms<T>(xr, cols, red, &M, &S);
+  if (threadIdx.x == 0) loss[blockIdx.x] = ce_row_loss<T>(xr, tgt[blockIdx.x], cols, ignore_index, M, S);
 }
 
 template <typename T>
@@ -629,13 +716,13 @@ static int launch_ce(const void* logits, const int64_t* tgt, float* loss, void* 
       ce_rows<T, L, VPT><<<grid, RowGeom<L>::kThreads, 0, s>>>(xp, tgt, loss, rows, (int)vocab, ignore_index);
     });
   }
+  // 16-bit rows that do not vectorise: the streaming kernel at any width past 4096 (measured, f16:
+  // 8192 x 50257 152.5 us against 216.1 register-cached packed and 274.1 fp32-cached; 4096 x 16385
+  // 33.0 against 80.1). For rows that vectorise the register-cached ce_rows stays faster (4096 x
+  // 32000: 51.6 against 57.1 streaming).
   if constexpr (sizeof(S) == 2) {
-    if (!handled && vocab > 4096 && vocab <= 64 * kWideThreads) {
-      const uint16_t* xs = (const uint16_t*)logits;
-      if (vocab <= 16 * kWideThreads)
-        ce_wide_pairs<T, 8><<<(unsigned)rows, kWideThreads, 0, s>>>(xs, tgt, loss, (int)vocab, ignore_index);
-      else
-        ce_wide_pairs<T, 32><<<(unsigned)rows, kWideThreads, 0, s>>>(xs, tgt, loss, (int)vocab, ignore_index);
+    if (!handled && vocab > 4096) {
+      ce_stream<T><<<(unsigned)rows, kLoopThreads, 0, s>>>((const uint16_t*)logits, tgt, loss, (int)vocab, ignore_index);
       handled = true;
     }
   }
