@@ -451,6 +451,19 @@ def test_softmax_ce_wide_odd_rows(gpu, cols, dtype):
     out_inf = ce(x.to(gpu), tg.to(gpu))
     assert math.isinf(out_inf.float().item()) and math.isinf(R.cross_entropy_ref(x, tg).float().item())
     assert torch.equal(out, ce(x[keep].to(gpu), tg[keep].to(gpu))), "cross-entropy wide rerun differs"
+    # a NaN or +inf logit makes its row NaN (softmax) and the loss NaN, as the oracle gives; an
+    # all -inf row is NaN too. Row 5 keeps a finite target so only the planted value matters.
+    xs = x[[0, 5, 0]].clone()
+    xs[0, cols // 2] = math.nan
+    xs[1, cols - 1] = math.inf
+    xs[2] = -math.inf
+    ys = sm(xs.to(gpu)).cpu()
+    ref = R.softmax_ref(xs)
+    assert torch.equal(torch.isnan(ys), torch.isnan(ref)), f"softmax wide {cols} {dtype}: NaN rows differ"
+    for r in range(3):
+        lr = ce(xs[r:r + 1].to(gpu), tg[[0]].to(gpu)).float().item()
+        er = R.cross_entropy_ref(xs[r:r + 1], tg[[0]]).float().item()
+        assert math.isnan(lr) and math.isnan(er), (cols, dtype, r, lr, er)
 
 
 def test_cross_entropy_ignore_and_3d(gpu):
