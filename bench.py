@@ -240,6 +240,30 @@ def e2e(timed: int = 20, warm: int = 3):
     return res
 
 
+def e2e_plugins(timed: int = 20, warm: int = 3):
+    """GPT-2 small [2, 1024] and BERT-base [8, 512] in f16 (seeded N(0, 0.02) weights): stock
+    PyTorch against every op the plug-in swaps (biased Linear, LayerNorm, attention), checked at the
+    north star's 1e-2."""
+    import torch
+    from autokernel_amd import bert, gpt2, verify
+    dev = torch.device("cuda:0")
+    res = []
+    for name, mod, shape in (("GPT-2 small (12 x 768, vocab 50257)", gpt2, (2, 1024)),
+                             ("BERT-base (12 x 768, FFN 3072), pooled output", bert, (8, 512))):
+        model = mod.build(torch.float16, dev)
+        ids = verify.make_token_ids(model, shape, dev)
+        ref_out, ref_ms = verify.benchmark_model(model, ids, warm, timed)
+        with verify.OptimizedModelContext(model, verify.ALL_KERNELS) as m:
+            opt_out, opt_ms = verify.benchmark_model(m, ids, warm, timed)
+        cmp = verify.compare_outputs(ref_out, opt_out, torch.float16, 1e-2, 1e-2)
+        res.append({"model": name, "input": list(shape), "dtype": "f16", "torch_ms": round(ref_ms, 3),
+                    "ak_ms": round(opt_ms, 3), "speedup": round(ref_ms / opt_ms, 3),
+                    "vs_stock_allclose_1e-2": cmp["correctness"], "vs_stock_max_abs": cmp.get("max_abs_error")})
+        del model, ref_out, opt_out
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(seconds: float):
     """The CPU oracle on a bounded sample of one step: 4 of 32 heads of q and k, 1024 of 8192 rows."""
     import torch
@@ -326,7 +350,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-ops", action="store_true", help="skip the per-op table")
-    ap.add_argument("--no-e2e", action="store_true", help="skip the LLaMA-7B forward")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the model forwards (LLaMA-7B, GPT-2, BERT)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -369,6 +393,13 @@ def main() -> int:
             log(f"  {out['e2e']}")
         except Exception as e:  # noqa: BLE001 - report, keep the headline
             out["e2e"] = {"error": f"{type(e).__name__}: {e}"}
+        try:
+            log("GPT-2 / BERT forwards:")
+            out["e2e_plugins"] = e2e_plugins()
+            for r in out["e2e_plugins"]:
+                log(f"  {r}")
+        except Exception as e:  # noqa: BLE001 - report, keep the headline
+            out["e2e_plugins"] = {"error": f"{type(e).__name__}: {e}"}
     if args.cpu_seconds > 0:
         log("cpu baseline:")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
