@@ -274,7 +274,12 @@ def flash_attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, causal: b
         Dp = 64 if D < 64 else 128
         padded = [torch.nn.functional.pad(t, (0, Dp - D)) for t in (Q, K, V)]
         return flash_attention(*padded, causal, scale)[..., :D].contiguous()
-    O = torch.empty((B, Hq, Sq, D), device=Q.device, dtype=Q.dtype)
+    if Q.is_contiguous():
+        O = torch.empty((B, Hq, Sq, D), device=Q.device, dtype=Q.dtype)
+    else:
+        # Q is a view of a model's [B, S, H, D] projection: O is written in that order too, so the
+        # caller's transpose back to [B, S, H * D] is a view rather than a copy (stock SDPA's layout)
+        O = torch.empty((B, Sq, Hq, D), device=Q.device, dtype=Q.dtype).transpose(1, 2)
     ops.flash_attn_fwd(O, _attn_operand(Q), _attn_operand(K), _attn_operand(V), bool(causal), scale)
     return O
 

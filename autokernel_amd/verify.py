@@ -431,8 +431,9 @@ class EncoderAttentionWrapper(nn.Module):
         def proj(lin, t):
             return _linear(t, lin.weight, lin.bias) if self.use_matmul else lin(t)
         q, k, v = (proj(lin, x).view(B, T, H, D) for lin in (o.query, o.key, o.value))
-        y = fa_mod.attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), False, None)
-        y = y.transpose(1, 2).reshape(B, T, C)
+        y = torch.empty((B, T, H, D), device=x.device, dtype=x.dtype)  # written in place, no transpose copy
+        fa_mod.attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), False, None, out=y.transpose(1, 2))
+        y = y.view(B, T, C)
         out = proj(o.out_proj, y)
         return o.dropout(out) if isinstance(getattr(o, "dropout", None), nn.Module) else out
 
@@ -458,7 +459,9 @@ class FusedQKVAttentionWrapper(nn.Module):
             return _linear(t, lin.weight, lin.bias) if self.use_matmul else lin(t)
         qkv = proj(o.c_attn, x)
         q, k, v = (qkv[..., i * C:(i + 1) * C].view(B, T, H, D).transpose(1, 2) for i in range(3))
-        y = fa_mod.attention(q, k, v, True, None).transpose(1, 2).reshape(B, T, C)
+        y = torch.empty((B, T, H, D), device=x.device, dtype=x.dtype)  # written in place, no transpose copy
+        fa_mod.attention(q, k, v, True, None, out=y.transpose(1, 2))
+        y = y.view(B, T, C)
         out = proj(o.c_proj, y)
         drop = getattr(o, "resid_dropout", None)
         return drop(out) if isinstance(drop, nn.Module) else out
