@@ -44,6 +44,8 @@ SIGNATURES: dict[str, list] = {
     "ak_gemm": [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],
     "ak_gemm_residual": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],
     "ak_gemm_bias": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],
+    "ak_gemm_bias_gelu": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],
+    "ak_gemm_bias_residual": [_i, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],
     "ak_gemm_workspace_bytes": [_i, _i64, _i64, _i64, _i64, _i64, _i64, _i],
     "ak_gemm_ws": [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p, _i64, _p],
     "ak_gemm_rope": [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p, _p, _i64, _i64, _i64, _p],

@@ -44,13 +44,23 @@ struct TF32 {
   __device__ __forceinline__ static void set_elem(u32x4& v, int i, float f) { v[i] = __float_as_uint(f); }
 };
 
+// The fp32 value is made opaque before a conversion to f16: hipcc otherwise folds a multiply, fma
+// or add that feeds the conversion into v_fma_mixlo_f16, which rounds the exact result to f16
+// once. A torch op rounds to fp32 first and then to f16; the two differ where the fp32 value
+// lies exactly halfway between two f16 values (gelu(-1.4853515625) is one). The empty asm emits
+// no instruction and, not being volatile, does not constrain scheduling.
+__device__ __forceinline__ float f32_opaque(float f) {
+  asm("" : "+v"(f));
+  return f;
+}
+
 struct TF16 {
   using S = uint16_t;
   static constexpr int kVec = 8;
   static constexpr int kCode = AK_F16;
   __device__ __forceinline__ static float to_f(S v) { return (float)__builtin_bit_cast(_Float16, v); }
-  __device__ __forceinline__ static S from_f(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
-  __device__ __forceinline__ static float rnd(float f) { return (float)(_Float16)f; }
+  __device__ __forceinline__ static S from_f(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f32_opaque(f)); }
+  __device__ __forceinline__ static float rnd(float f) { return (float)(_Float16)f32_opaque(f); }
   __device__ __forceinline__ static float lane_elem(const u32x4& v, int i) {
     uint32_t w = v[i >> 1];
     return to_f((S)((i & 1) ? (w >> 16) : (w & 0xffffu)));

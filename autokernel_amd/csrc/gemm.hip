@@ -109,7 +109,7 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int* tm, i
 // Epilogues (applied to fp32 accumulators; every step rounds like the reference's tensor ops)
 // --------------------------------------------------------------------------------------------
 enum Epi { kEpiStore = 0, kEpiSilu = 1, kEpiGelu = 2, kEpiRelu2 = 3, kEpiNone = 4, kEpiResidual = 5, kEpiRope = 6,
-           kEpiPartial = 7, kEpiBias = 8 };
+           kEpiPartial = 7, kEpiBias = 8, kEpiBiasGelu = 9, kEpiBiasResidual = 10 };
 
 // Arguments of the rotary epilogue (kEpiRope), passed by value to every f16 / bf16 GEMM kernel:
 // columns [0, rot_cols) of C form heads of head_dim columns whose (even, odd) pairs are rotated
@@ -119,6 +119,7 @@ enum Epi { kEpiStore = 0, kEpiSilu = 1, kEpiGelu = 2, kEpiRelu2 = 3, kEpiNone = 
 // by z * split_a / z * split_b elements and stores its fp32 accumulators to the workspace advanced by
 // z * split_c floats (row stride ldc), for splitk_reduce to sum.
 struct EpiArgs {
+  const uint16_t* bias = nullptr;  // kEpiBiasResidual (R is the residual there)
   const float* cos = nullptr;
   const float* sin = nullptr;
   int head_dim = 0;
@@ -138,13 +139,16 @@ __device__ __forceinline__ void rope_rotate(float& a, float& b, float c, float s
   b = y2;
 }
 
+// torch's exact GELU of one rounded value, in fp32: x * 0.5 * (1 + erf(x / sqrt(2)))
+__device__ __forceinline__ float gelu_erf(float g) { return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f)); }
+
 template <typename T, int EPI>
 __device__ __forceinline__ float gate_up(float g_acc, float u_acc) {
   const float g = T::rnd(g_acc);
   const float u = T::rnd(u_acc);
   float a;
   if constexpr (EPI == kEpiSilu) a = T::rnd(g / (1.0f + expf(-g)));
-  else if constexpr (EPI == kEpiGelu) a = T::rnd(0.5f * g * (1.0f + erff(g * 0.70710678118654752f)));
+  else if constexpr (EPI == kEpiGelu) a = T::rnd(gelu_erf(g));
   else if constexpr (EPI == kEpiRelu2) { const float r = g > 0.f ? g : 0.f; a = T::rnd(r * r); }
   else a = g;
   return a * u;  // rounded by the store
@@ -159,6 +163,10 @@ __device__ __forceinline__ float gate_up(float g_acc, float u_acc) {
 //     gives the correctly rounded sum.
 //   kEpiBias adds bias[n + e] (the element type, R points at it) to the fp32 accumulator and
 //     rounds once: nn.Linear's fused bias (torch's addmm adds it in the fp32 compute type).
+//   kEpiBiasGelu is kEpiBias's rounded value through exact GELU in fp32, rounded again: a biased
+//     nn.Linear followed by nn.GELU (R points at the bias).
+//   kEpiBiasResidual is kEpiBias's rounded value plus R[m][n + e] (the residual; the bias comes
+//     from ep.bias), rounded again: torch's `R + linear(x)` for a biased Linear.
 //   kEpiRope rounds the product to the element type, then (columns below rot_cols) rotates the
 //     pairs (n, n + 1), (n + 2, n + 3) in fp32 by table row m % seq_len and rounds once: the
 //     projection's output cast to fp32, rotated and cast back. n is a multiple of 4 and head_dim
@@ -171,9 +179,9 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
                                               int64_t ldc, int M, int N, int mb, int nb,
                                               const f32x4 (&acc)[NB][FM][FN], const EpiArgs& ep) {
   typedef float f32x2 __attribute__((ext_vector_type(2)));
-  constexpr bool kRes = NB == 1 && EPI == kEpiResidual;
+  constexpr bool kRes = NB == 1 && (EPI == kEpiResidual || EPI == kEpiBiasResidual);
   constexpr bool kRope = NB == 1 && EPI == kEpiRope;
-  constexpr bool kBias = NB == 1 && EPI == kEpiBias;
+  constexpr bool kBias = NB == 1 && (EPI == kEpiBias || EPI == kEpiBiasGelu || EPI == kEpiBiasResidual);
   if constexpr (NB == 1 && EPI == kEpiPartial) {
     // fp32 accumulators as they are (C is the fp32 workspace; N % 4 == 0 and ldc % 4 == 0)
     float* Cf = reinterpret_cast<float*>(C);
@@ -192,11 +200,12 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
   u32x2 side_r[kRes ? FM : 1][kRes ? FN : 1];
   float side_b[kBias ? FN : 1][4];
   if constexpr (kBias) {
+    const uint16_t* bias = EPI == kEpiBiasResidual ? ep.bias : R;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int n = nb + j * NST;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) side_b[j][e] = n + e < N ? T::to_f(R[n + e]) : 0.f;
+      for (int e = 0; e < 4; ++e) side_b[j][e] = n + e < N ? T::to_f(bias[n + e]) : 0.f;
     }
   }
   f32x2 side_c[kRope ? FM : 1][kRope ? FN : 1], side_s[kRope ? FM : 1][kRope ? FN : 1];
@@ -251,16 +260,20 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         if constexpr (NB == 2) v[e] = gate_up<T, EPI>(acc[0][i][j][e], acc[1][i][j][e]);
-        else if constexpr (kRes || kRope) v[e] = T::rnd(acc[0][i][j][e]);
+        else if constexpr ((kRes && !kBias) || kRope) v[e] = T::rnd(acc[0][i][j][e]);
         else v[e] = acc[0][i][j][e];
+      }
+      if constexpr (kBias) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] += side_b[j][e];
+          if constexpr (EPI != kEpiBias) v[e] = T::rnd(v[e]);
+          if constexpr (EPI == kEpiBiasGelu) v[e] = gelu_erf(v[e]);
+        }
       }
       if constexpr (kRes) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] += T::to_f((uint16_t)(side_r[i][j][e >> 1] >> ((e & 1) * 16)));
-      }
-      if constexpr (kBias) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] += side_b[j][e];
       }
       if constexpr (kRope) {
         if (n < ep.rot_cols) {
@@ -979,7 +992,7 @@ static int launch_gemm16(const void* A, const void* B0, const void* B1, void* C,
                          int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, bool bt,
                          hipStream_t s, const EpiArgs& ep = EpiArgs{}) {
   bool vec = K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && host_aligned16(A) &&
-             host_aligned16(B0) && (!B1 || EPI == kEpiBias || host_aligned16(B1)) && (((uintptr_t)C) & 7u) == 0;
+             host_aligned16(B0) && (!B1 || EPI == kEpiBias || EPI == kEpiBiasGelu || host_aligned16(B1)) && (((uintptr_t)C) & 7u) == 0;
   if (!bt) vec = vec && N % 8 == 0;
   const int m = (int)M, n = (int)N, k = (int)K;
   // LDS-DMA path: nn.Linear-layout B, K a multiple of 64, 32-bit element offsets
@@ -1252,6 +1265,46 @@ extern "C" int ak_gemm_bias(int dtype, const void* A, const void* B, const void*
   switch (dtype) {
     case AK_F16: return launch_gemm16<TF16, 1, kEpiBias>(A, B, bias, C, M, N, K, lda, ldb, ldc, bt, stream);
     case AK_BF16: return launch_gemm16<TBF16, 1, kEpiBias>(A, B, bias, C, M, N, K, lda, ldb, ldc, bt, stream);
+    case AK_F32: return AK_EUNSUPPORTED;
+    default: return AK_EINVAL;
+  }
+}
+
+extern "C" int ak_gemm_bias_gelu(int dtype, const void* A, const void* B, const void* bias, void* C, int64_t M,
+                                 int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int b_trans,
+                                 hipStream_t stream) {
+  if (M < 0 || N < 0 || K < 0 || M > INT_MAX || N > INT_MAX || K > INT_MAX) return AK_EINVAL;
+  if (M == 0 || N == 0) return AK_OK;
+  if (!A || !B || !bias || !C) return AK_EINVAL;
+  if (lda < K || ldc < N || ldb < (b_trans ? K : N)) return AK_EINVAL;
+  if (cdiv(M, 128) * cdiv(N, 128) > INT_MAX) return AK_EINVAL;
+  const bool bt = b_trans != 0;
+  switch (dtype) {
+    case AK_F16: return launch_gemm16<TF16, 1, kEpiBiasGelu>(A, B, bias, C, M, N, K, lda, ldb, ldc, bt, stream);
+    case AK_BF16: return launch_gemm16<TBF16, 1, kEpiBiasGelu>(A, B, bias, C, M, N, K, lda, ldb, ldc, bt, stream);
+    case AK_F32: return AK_EUNSUPPORTED;
+    default: return AK_EINVAL;
+  }
+}
+
+extern "C" int ak_gemm_bias_residual(int dtype, const void* A, const void* B, const void* bias, const void* R,
+                                     void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                                     int64_t ldc, int b_trans, hipStream_t stream) {
+  if (M < 0 || N < 0 || K < 0 || M > INT_MAX || N > INT_MAX || K > INT_MAX) return AK_EINVAL;
+  if (M == 0 || N == 0) return AK_OK;
+  if (!A || !B || !bias || !R || !C) return AK_EINVAL;
+  if (lda < K || ldc < N || ldb < (b_trans ? K : N)) return AK_EINVAL;
+  if (cdiv(M, 128) * cdiv(N, 128) > INT_MAX) return AK_EINVAL;
+  // R is read and C written element by element in one pass: they must not overlap
+  const uintptr_t r0 = (uintptr_t)R, c0 = (uintptr_t)C;
+  const uintptr_t span = (uintptr_t)(((M - 1) * ldc + N) * 2);
+  if (r0 < c0 + span && c0 < r0 + span) return AK_EINVAL;
+  const bool bt = b_trans != 0;
+  EpiArgs ep;
+  ep.bias = (const uint16_t*)bias;
+  switch (dtype) {
+    case AK_F16: return launch_gemm16<TF16, 1, kEpiBiasResidual>(A, B, R, C, M, N, K, lda, ldb, ldc, bt, stream, ep);
+    case AK_BF16: return launch_gemm16<TBF16, 1, kEpiBiasResidual>(A, B, R, C, M, N, K, lda, ldb, ldc, bt, stream, ep);
     case AK_F32: return AK_EUNSUPPORTED;
     default: return AK_EINVAL;
   }

@@ -100,6 +100,25 @@ def gemm_bias(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor, bias: torch.Ten
          _ld(a), _ld(b), _ld(c), int(bool(b_trans)), M=M, N=N, K=K, b_trans=b_trans, dtype=a.dtype)
 
 
+def gemm_bias_gelu(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor, b_trans: bool) -> None:
+    """c = gelu(a @ op(b) + bias): the biased product rounded, then exact GELU, rounded again."""
+    M, K = a.shape
+    N = b.shape[0] if b_trans else b.shape[1]
+    _run("ak_gemm_bias_gelu", a, _code(a, "gemm_bias_gelu"), a.data_ptr(), b.data_ptr(), bias.data_ptr(),
+         c.data_ptr(), M, N, K, _ld(a), _ld(b), _ld(c), int(bool(b_trans)), M=M, N=N, K=K, b_trans=b_trans,
+         dtype=a.dtype)
+
+
+def gemm_bias_residual(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor, r: torch.Tensor,
+                       b_trans: bool) -> None:
+    """c = r + (a @ op(b) + bias): the biased product rounded, then the sum (r shares c's row stride)."""
+    M, K = a.shape
+    N = b.shape[0] if b_trans else b.shape[1]
+    _run("ak_gemm_bias_residual", a, _code(a, "gemm_bias_residual"), a.data_ptr(), b.data_ptr(), bias.data_ptr(),
+         r.data_ptr(), c.data_ptr(), M, N, K, _ld(a), _ld(b), _ld(c), int(bool(b_trans)), M=M, N=N, K=K,
+         b_trans=b_trans, dtype=a.dtype)
+
+
 def gemm_residual(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor, r: torch.Tensor, b_trans: bool) -> None:
     """c = r + a @ op(b), the product rounded, then the sum (r shares c's row stride)."""
     M, K = a.shape

@@ -6,8 +6,8 @@ row-major [N, K] tensor (nn.Linear's weight.t()), the GEMM reads it in place (b_
 instead of copying; a row-major [K, N] B is read in place too (b_trans = 0). Runs ak_gemm
 (gemm.hip), or, for kernel_fn, ak_gemm_ws with a torch-allocated fp32 workspace when few output tiles
 and a long K would leave most CUs idle (K split into slices that run side by side, then added in a
-fixed order). kernel_fn is kernels/host.py's matmul; gemm, gemm_bias, gemm_residual and
-gemm_rope are the 2-D forms (and fused epilogues) the model plug-in uses.
+fixed order). kernel_fn is kernels/host.py's matmul; gemm, gemm_bias, gemm_bias_gelu, gemm_bias_residual,
+gemm_residual and gemm_rope are the 2-D forms (and fused epilogues) the model plug-in uses.
 """
 from __future__ import annotations
 
@@ -55,15 +55,46 @@ def _epilogue_operands(op: str, A: torch.Tensor, B: torch.Tensor):
     return _a_rows(A), Bs, bt, M, N
 
 
+def _bias_operand(op: str, bias: torch.Tensor, A: torch.Tensor, N: int) -> torch.Tensor:
+    if tuple(bias.shape) != (N,) or bias.dtype != A.dtype:
+        raise ValueError(f"{op}: bias {tuple(bias.shape)} {bias.dtype} does not fit [{N}] {A.dtype}")
+    return bias.contiguous()
+
+
 def gemm_bias(A: torch.Tensor, B: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
     """A @ B + bias for 2-D A [M, K], B [K, N] (a transposed [N, K] view is read in place) and
     bias [N], f16 / bf16, in one ak_gemm_bias launch: the bias joins the fp32 accumulator and the
     sum is rounded once, as torch's addmm (a biased nn.Linear) rounds it."""
     A, Bs, bt, M, N = _epilogue_operands("gemm_bias", A, B)
-    if tuple(bias.shape) != (N,) or bias.dtype != A.dtype:
-        raise ValueError(f"gemm_bias: bias {tuple(bias.shape)} {bias.dtype} does not fit [{N}] {A.dtype}")
+    bias = _bias_operand("gemm_bias", bias, A, N)
     C = torch.empty((M, N), device=A.device, dtype=A.dtype)
-    _ops.gemm_bias(C, A, Bs, bias.contiguous(), bt)
+    _ops.gemm_bias(C, A, Bs, bias, bt)
+    return C
+
+
+def gemm_bias_gelu(A: torch.Tensor, B: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """gelu(A @ B + bias) (exact erf GELU) for 2-D A [M, K], B [K, N] (a transposed [N, K] view is
+    read in place) and bias [N], f16 / bf16, in one ak_gemm_bias_gelu launch: the biased product is
+    rounded as gemm_bias rounds it, then GELU in fp32 is rounded again, as a biased nn.Linear
+    followed by nn.GELU computes it (models/gpt2.py:60-62, models/bert_base.py:47-48)."""
+    A, Bs, bt, M, N = _epilogue_operands("gemm_bias_gelu", A, B)
+    bias = _bias_operand("gemm_bias_gelu", bias, A, N)
+    C = torch.empty((M, N), device=A.device, dtype=A.dtype)
+    _ops.gemm_bias_gelu(C, A, Bs, bias, bt)
+    return C
+
+
+def gemm_bias_residual(A: torch.Tensor, B: torch.Tensor, bias: torch.Tensor, R: torch.Tensor) -> torch.Tensor:
+    """R + (A @ B + bias) for 2-D A [M, K], B [K, N] (a transposed [N, K] view is read in place),
+    bias [N] and R [M, N], f16 / bf16, in one ak_gemm_bias_residual launch: the biased product is
+    rounded, then the add, so the result equals torch's `R + linear(x)` for a biased Linear bit for
+    bit (models/gpt2.py:63-65, models/bert_base.py:60-62)."""
+    A, Bs, bt, M, N = _epilogue_operands("gemm_bias_residual", A, B)
+    bias = _bias_operand("gemm_bias_residual", bias, A, N)
+    if tuple(R.shape) != (M, N) or R.dtype != A.dtype:
+        raise ValueError(f"gemm_bias_residual: R {tuple(R.shape)} {R.dtype} does not fit [{M}, {N}] {A.dtype}")
+    C = torch.empty((M, N), device=A.device, dtype=A.dtype)
+    _ops.gemm_bias_residual(C, A, Bs, bias, R.contiguous(), bt)
     return C
 
 

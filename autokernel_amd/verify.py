@@ -52,7 +52,7 @@ from . import kernels
 from .kernels import flash_attention as fa_mod
 from .kernels import rotary_embedding as rope_mod
 from .kernels.fused_mlp import gate_up
-from .kernels.matmul import gemm, gemm_bias, gemm_residual, gemm_rope
+from .kernels.matmul import gemm, gemm_bias, gemm_bias_gelu, gemm_bias_residual, gemm_residual, gemm_rope
 from .kernels.rmsnorm import rms_norm_rsqrt
 
 ALL_KERNELS = ("matmul", "rmsnorm", "layernorm", "rotary_embedding", "flash_attention", "fused_mlp")
@@ -293,6 +293,55 @@ def _fusable(residual: torch.Tensor) -> bool:
     return residual.dtype in (torch.float16, torch.bfloat16)
 
 
+def _identity_dropout(d) -> bool:
+    """A missing dropout, or one that passes its input through (eval mode or p = 0)."""
+    return not isinstance(d, nn.Dropout) or not d.training or d.p == 0
+
+
+def _bias_fusable(lin: nn.Linear, x: torch.Tensor) -> bool:
+    """The biased-GEMM epilogues serve an f16 / bf16 Linear whose bias has the input's dtype."""
+    return _fusable(x) and lin.bias is not None and lin.bias.dtype == x.dtype and lin.weight.dtype == x.dtype
+
+
+def _linear_residual(x: torch.Tensor, lin: nn.Linear, residual: Optional[torch.Tensor]) -> torch.Tensor:
+    """residual + lin(x), the add carried by the GEMM's epilogue where the dtypes allow: the
+    product (+ bias) is rounded, then the sum, as the separate add rounds it."""
+    if residual is None:
+        return _linear(x, lin.weight, lin.bias)
+    x2 = x.reshape(-1, x.shape[-1])
+    r2 = residual.reshape(-1, residual.shape[-1])
+    if _bias_fusable(lin, x):
+        return gemm_bias_residual(x2, lin.weight.t(), lin.bias, r2).view(residual.shape)
+    if lin.bias is None and _fusable(x):
+        return gemm_residual(x2, lin.weight.t(), r2).view(residual.shape)
+    return residual + _linear(x, lin.weight, lin.bias)
+
+
+class GeluMLPWrapper(nn.Module):
+    """proj(gelu(fc(x))) (+ dropout), the two-Linear GELU MLP of the reference's GPT-2 (c_fc / c_proj,
+    models/gpt2.py:55-68) and BERT (dense1 / dense2, models/bert_base.py:43-53), in two GEMM launches:
+    fc's bias and the exact (erf) GELU in the first GEMM's epilogue, proj's bias (and a caller's
+    residual) in the second's. Each intermediate is rounded where the stock modules round it, so the
+    output matches them bit for bit. Other dtypes, a tanh GELU or an active dropout take the
+    unfused path (libak355 GEMMs, the module's own GELU and dropout)."""
+
+    def __init__(self, original: nn.Module, fc: nn.Linear, gelu: nn.GELU, proj: nn.Linear):
+        super().__init__()
+        self.original = original
+        self.fc, self.gelu, self.proj = fc, gelu, proj
+        drops = [c for c in original.children() if isinstance(c, nn.Dropout)]
+        self.drop = drops[0] if drops else None
+
+    def forward(self, x, residual: Optional[torch.Tensor] = None):
+        fc, proj = self.fc, self.proj
+        if not (_bias_fusable(fc, x) and self.gelu.approximate == "none" and _identity_dropout(self.drop)):
+            y = _linear(self.gelu(_linear(x, fc.weight, fc.bias)), proj.weight, proj.bias)
+            y = self.drop(y) if self.drop is not None else y
+            return y if residual is None else residual + y
+        h = gemm_bias_gelu(x.reshape(-1, x.shape[-1]), fc.weight.t(), fc.bias)
+        return _linear_residual(h.view(*x.shape[:-1], -1), proj, residual)
+
+
 def _rope_tables_from(args) -> Tuple[torch.Tensor, torch.Tensor]:
     """cos / sin from either (cos, sin) tensors or one complex freqs_cis tensor."""
     if len(args) >= 2 and not torch.is_complex(args[0]):
@@ -420,10 +469,11 @@ class EncoderAttentionWrapper(nn.Module):
         self.original = original
         self.use_matmul = use_matmul
 
-    def forward(self, x, attention_mask=None):
+    def forward(self, x, attention_mask=None, residual: Optional[torch.Tensor] = None):
         o = self.original
         if attention_mask is not None:
-            return o(x, attention_mask)
+            out = o(x, attention_mask)
+            return out if residual is None else residual + out
         B, T, C = x.shape
         H = o.num_heads
         D = C // H
@@ -434,8 +484,12 @@ class EncoderAttentionWrapper(nn.Module):
         y = torch.empty((B, T, H, D), device=x.device, dtype=x.dtype)  # written in place, no transpose copy
         fa_mod.attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), False, None, out=y.transpose(1, 2))
         y = y.view(B, T, C)
+        drop = getattr(o, "dropout", None)
+        if residual is not None and self.use_matmul and _identity_dropout(drop):
+            return _linear_residual(y, o.out_proj, residual)
         out = proj(o.out_proj, y)
-        return o.dropout(out) if isinstance(getattr(o, "dropout", None), nn.Module) else out
+        out = drop(out) if isinstance(drop, nn.Module) else out
+        return out if residual is None else residual + out
 
 
 class FusedQKVAttentionWrapper(nn.Module):
@@ -449,7 +503,7 @@ class FusedQKVAttentionWrapper(nn.Module):
         self.original = original
         self.use_matmul = use_matmul
 
-    def forward(self, x):
+    def forward(self, x, residual: Optional[torch.Tensor] = None):
         o = self.original
         B, T, C = x.shape
         H = o.n_head
@@ -462,9 +516,12 @@ class FusedQKVAttentionWrapper(nn.Module):
         y = torch.empty((B, T, H, D), device=x.device, dtype=x.dtype)  # written in place, no transpose copy
         fa_mod.attention(q, k, v, True, None, out=y.transpose(1, 2))
         y = y.view(B, T, C)
-        out = proj(o.c_proj, y)
         drop = getattr(o, "resid_dropout", None)
-        return drop(out) if isinstance(drop, nn.Module) else out
+        if residual is not None and self.use_matmul and _identity_dropout(drop):
+            return _linear_residual(y, o.c_proj, residual)
+        out = proj(o.c_proj, y)
+        out = drop(out) if isinstance(drop, nn.Module) else out
+        return out if residual is None else residual + out
 
 
 class ResidualBlockWrapper(nn.Module):
@@ -483,9 +540,65 @@ class ResidualBlockWrapper(nn.Module):
         return b.feed_forward(b.ffn_norm(h), residual=h)
 
 
+class GPT2BlockWrapper(nn.Module):
+    """Pre-norm block x = x + attn(ln_1(x)); x = x + mlp(ln_2(x)) (models/gpt2.py:71-82) whose attn
+    and mlp are libak355 wrappers: each residual add is carried by the epilogue of the GEMM that
+    ends its branch (c_proj of the attention, c_proj of the MLP), bit for bit the separate add."""
+
+    def __init__(self, original: nn.Module):
+        super().__init__()
+        self.original = original
+
+    def forward(self, x):
+        b = self.original
+        h = b.attn(b.ln_1(x), residual=x)
+        return b.mlp(b.ln_2(h), residual=h)
+
+
+class PostNormBlockWrapper(nn.Module):
+    """Post-norm block x = norm1(x + attention(x)); x = norm2(x + mlp(x)) (models/bert_base.py:56-66)
+    whose attention and mlp are libak355 wrappers: each residual add is carried by the epilogue of
+    the GEMM that ends its branch (out_proj, dense2), the norms by the layernorm strategy or stock."""
+
+    def __init__(self, original: nn.Module):
+        super().__init__()
+        self.original = original
+
+    def forward(self, x):
+        b = self.original
+        h = b.norm1(b.attention(x, residual=x))
+        return b.norm2(b.mlp(h, residual=h))
+
+
 def _is_prenorm_block(m: nn.Module) -> bool:
     return all(isinstance(getattr(m, n, None), nn.Module)
                for n in ("attention", "feed_forward", "attention_norm", "ffn_norm"))
+
+
+def _is_gpt2_block(m: nn.Module) -> bool:
+    return (all(isinstance(getattr(m, n, None), nn.Module) for n in ("ln_1", "attn", "ln_2", "mlp"))
+            and isinstance(m.attn, FusedQKVAttentionWrapper) and m.attn.use_matmul
+            and isinstance(m.mlp, GeluMLPWrapper))
+
+
+def _is_postnorm_block(m: nn.Module) -> bool:
+    return (all(isinstance(getattr(m, n, None), nn.Module) for n in ("attention", "norm1", "mlp", "norm2"))
+            and not hasattr(m, "feed_forward") and isinstance(m.attention, EncoderAttentionWrapper)
+            and m.attention.use_matmul and isinstance(m.mlp, GeluMLPWrapper))
+
+
+def _gelu_mlp_parts(m: nn.Module):
+    """(fc, gelu, proj) of a Linear -> GELU -> Linear MLP named as GPT-2's (c_fc, c_proj) or BERT's
+    (dense1, dense2) with one nn.GELU child; None for anything else."""
+    gelus = [c for c in m.children() if isinstance(c, nn.GELU)]
+    if len(gelus) != 1:
+        return None
+    for a, b in (("c_fc", "c_proj"), ("dense1", "dense2")):
+        fc, proj = getattr(m, a, None), getattr(m, b, None)
+        if (isinstance(fc, nn.Linear) and isinstance(proj, nn.Linear) and fc.out_features == proj.in_features
+                and fc.in_features == proj.out_features):
+            return fc, gelus[0], proj
+    return None
 
 
 # ------------------------------------------------------------------------- module swapping
@@ -602,6 +715,10 @@ class OptimizedModelContext:
                 self._set(name, FeedForwardWrapper(m, *_swiglu_parts(m)))
                 taken.update(n for n, _ in m.named_modules(prefix=name))
                 self._count("fused_mlp")
+            elif "matmul" in k and _gelu_mlp_parts(m) is not None:
+                self._set(name, GeluMLPWrapper(m, *_gelu_mlp_parts(m)))
+                taken.update(n for n, _ in m.named_modules(prefix=name))
+                self._count("gelu_mlp")
         for name, m in modules:
             if not name or name in taken or any(name.startswith(t + ".") for t in taken):
                 continue
@@ -625,6 +742,12 @@ class OptimizedModelContext:
                 if (name and _is_prenorm_block(m) and isinstance(m.attention, AttentionWrapper)
                         and m.attention.use_matmul and isinstance(m.feed_forward, FeedForwardWrapper)):
                     self._set(name, ResidualBlockWrapper(m))
+                    self._count("residual_block")
+                elif name and _is_gpt2_block(m):
+                    self._set(name, GPT2BlockWrapper(m))
+                    self._count("residual_block")
+                elif name and _is_postnorm_block(m):
+                    self._set(name, PostNormBlockWrapper(m))
                     self._count("residual_block")
         return self.model
 

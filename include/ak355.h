@@ -210,6 +210,30 @@ int ak_gemm_bias(int dtype, const void* A, const void* B, const void* bias, void
                  hipStream_t stream);
 
 /*
+ * ak_gemm_bias followed by exact GELU: C = gelu(A * op(B) + bias), the biased product rounded to
+ * the element type as ak_gemm_bias rounds it, then x * 0.5 * (1 + erf(x / sqrt(2))) in fp32 and
+ * rounded again: nn.Linear then nn.GELU (torch's addmm, then its GELU kernel in fp32), bit for bit.
+ * Arguments as in ak_gemm_bias. f16 / bf16 (fp32: AK_EUNSUPPORTED).
+ * Replaces: models/gpt2.py:60-62 and models/bert_base.py:47-48 (c_fc / dense1 followed by the MLP's
+ *           GELU): the first MLP projection plus the GELU kernel that follows it.
+ */
+int ak_gemm_bias_gelu(int dtype, const void* A, const void* B, const void* bias, void* C, int64_t M,
+                      int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int b_trans,
+                      hipStream_t stream);
+
+/*
+ * ak_gemm_bias plus a residual: C = R + (A * op(B) + bias), the biased product rounded to the
+ * element type, R added and the sum rounded again: torch's `x + linear(y)` for a biased Linear, bit
+ * for bit. R [M, N] has C's row stride ldc and must not overlap C. f16 / bf16.
+ * Replaces: models/gpt2.py:63-65 (x + attn(...), x + mlp(...)) and models/bert_base.py:60-62
+ *           (x + attention(x), x + mlp(x) before each LayerNorm): the output projections' GEMM plus
+ *           the add kernel that follows it.
+ */
+int ak_gemm_bias_residual(int dtype, const void* A, const void* B, const void* bias, const void* R,
+                          void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                          int64_t ldc, int b_trans, hipStream_t stream);
+
+/*
  * GEMM with the model's rotary embedding in its epilogue: C = A * op(B) (arguments as in ak_gemm),
  * the product rounded to the element type; then, in columns [0, rot_cols), every head of head_dim
  * columns has its (even, odd) pairs rotated in fp32 by cos / sin [seq_len, head_dim / 2] (fp32,

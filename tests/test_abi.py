@@ -71,6 +71,15 @@ def test_invalid_arguments_rejected_on_host(lib):
     assert lib.ak_gemm_residual(1, x, x, None, y, 4, 4, 4, 4, 4, 4, 0, None) == _lib.AK_EINVAL
     assert lib.ak_gemm_residual(0, x, x, x, y, 4, 4, 4, 4, 4, 4, 0, None) == _lib.AK_EUNSUPPORTED  # fp32
     assert lib.ak_gemm_residual(1, x, x, x, y, 0, 4, 4, 4, 4, 4, 0, None) == _lib.AK_OK  # empty
+    assert lib.ak_gemm_bias_gelu(1, x, x, None, y, 4, 4, 4, 4, 4, 4, 1, None) == _lib.AK_EINVAL  # no bias
+    assert lib.ak_gemm_bias_gelu(1, x, x, x, y, 4, 4, 4, 4, 4, 2, 1, None) == _lib.AK_EINVAL     # ldc < N
+    assert lib.ak_gemm_bias_gelu(0, x, x, x, y, 4, 4, 4, 4, 4, 4, 1, None) == _lib.AK_EUNSUPPORTED  # fp32
+    assert lib.ak_gemm_bias_gelu(1, x, x, x, y, 4, 0, 4, 4, 4, 4, 1, None) == _lib.AK_OK         # empty
+    assert lib.ak_gemm_bias_residual(1, x, x, x, x, x, 4, 4, 4, 4, 4, 4, 1, None) == _lib.AK_EINVAL  # R is C
+    assert lib.ak_gemm_bias_residual(1, x, x, x, None, y, 4, 4, 4, 4, 4, 4, 1, None) == _lib.AK_EINVAL
+    assert lib.ak_gemm_bias_residual(1, x, x, None, x, y, 4, 4, 4, 4, 4, 4, 1, None) == _lib.AK_EINVAL
+    assert lib.ak_gemm_bias_residual(0, x, x, x, x, y, 4, 4, 4, 4, 4, 4, 1, None) == _lib.AK_EUNSUPPORTED
+    assert lib.ak_gemm_bias_residual(1, x, x, x, x, y, 0, 4, 4, 4, 4, 4, 1, None) == _lib.AK_OK  # empty
     assert lib.ak_gemm_workspace_bytes(1, 1024, 1024, 8192, 8192, 8192, 1024, 1) == 4 * 1024 * 1024 * 4
     assert lib.ak_gemm_workspace_bytes(1, 1024, 1024, 4096, 4096, 1024, 1024, 0) == 4 * 1024 * 1024 * 4
     assert lib.ak_gemm_workspace_bytes(1, 1024, 1024, 1024, 1024, 1024, 1024, 0) == 0   # slices < 1024 deep

@@ -700,3 +700,72 @@ def test_gemm_bias_one_rounding(gpu, M, N, K):
         eq = (out == stock).float().mean().item()
         print(f"gemm_bias {M}x{N}x{K} {dt}: {100 * eq:.3f}% bit-equal to F.linear", flush=True)
         assert eq > 0.99
+
+
+def _ulps16(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Distance in units in the last place between two f16 / bf16 tensors of one dtype (finite)."""
+    def ordered(t):
+        i = t.contiguous().view(torch.int16).int()
+        return torch.where(i < 0, -(i & 0x7FFF), i)
+    return (ordered(a) - ordered(b)).abs()
+
+
+def _gelu_matches_torch(out: torch.Tensor, exp: torch.Tensor, what: str) -> None:
+    """out against torch's F.gelu of the same rounded inputs: bit-equal on all but a handful of
+    elements, and within one unit in the last place everywhere. The exceptions are inputs whose fp32
+    GELU lies within a few fp32 ulps of a rounding tie of the element type (f16 x = -1.4853515625:
+    exact GELU -0.1020813206, the f16 midpoint -0.1020812988); 1 + erf(x / sqrt 2) cancels there, and
+    torch's own F.gelu on the GPU lands on either side of the tie depending on the element's
+    position in its vectorised loop."""
+    ulps = _ulps16(out, exp)
+    n_diff = int((ulps != 0).sum())
+    print(f"{what}: {n_diff} of {out.numel()} elements differ from F.gelu (max {int(ulps.max())} ulp)", flush=True)
+    assert int(ulps.max()) <= 1, what
+    assert n_diff <= max(4, out.numel() // 100000), what
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 3072, 768), (8 * 512, 768, 3072), (300, 520, 200), (257, 77, 96)])
+def test_gemm_bias_gelu_and_residual_epilogues(gpu, M, N, K):
+    """ak_gemm_bias_gelu and ak_gemm_bias_residual (GPT-2 / BERT MLP and output-projection shapes, an
+    unaligned N that takes the register-staged path), f16 and bf16: ak_gemm_bias followed by torch's
+    own F.gelu on the GPU to within the rounding-tie rule of _gelu_matches_torch, the residual form
+    bit-equal to ak_gemm_bias plus torch's add (the rounding points of a biased nn.Linear, nn.GELU
+    and `x + y`), and the GELU form within the harness's matmul tolerance (f16 1e-2, bf16 2e-2,
+    bench.py:330-337) of the oracle's fp32 product + bias, rounded, through exact GELU in fp32."""
+    from autokernel_amd.kernels.matmul import gemm_bias, gemm_bias_gelu, gemm_bias_residual
+    F = torch.nn.functional
+    for dt in (torch.float16, torch.bfloat16):
+        g = torch.Generator().manual_seed(M * 3 + N + K)
+        x = torch.randn(M, K, generator=g).to(dt)
+        W = (torch.randn(N, K, generator=g) * 0.05).to(dt)
+        b = (torch.randn(N, generator=g) * 0.5).to(dt)
+        r = torch.randn(M, N, generator=g).to(dt)
+        xd, Wd, bd, rd = x.to(gpu), W.to(gpu), b.to(gpu), r.to(gpu)
+        lin = gemm_bias(xd, Wd.t(), bd)
+        out = gemm_bias_gelu(xd, Wd.t(), bd)
+        _gelu_matches_torch(out, F.gelu(lin), f"gelu epilogue {M}x{N}x{K} {dt}")
+        exp = F.gelu((R.matmul_ref(x.float(), W.float().T) + b.float()).to(dt).float()).to(dt)
+        tol = spec.KERNEL_CONFIGS["matmul"]["tolerances"][dt]
+        assert_close(out, exp, tol["atol"], tol["rtol"], f"gemm_bias_gelu vs oracle {M}x{N}x{K} {dt}")
+        res = gemm_bias_residual(xd, Wd.t(), bd, rd)
+        assert torch.equal(res, rd + lin), f"residual epilogue {M}x{N}x{K} {dt}"
+        print(f"gemm bias+residual {M}x{N}x{K} {dt}: bit-equal", flush=True)
+
+
+def test_gemm_bias_gelu_every_value(gpu):
+    """Every finite f16 / bf16 value through ak_gemm_bias_gelu once: with A the [256, 256] identity
+    and a zero bias, C[m, n] = W[n, m] exactly, so W [N, 256] holding all finite values feeds each
+    to the epilogue. Matches F.gelu of the same values under _gelu_matches_torch's rule: the fp32
+    GELU is rounded like torch's (fp32 first, then the element type, never once from the exact
+    product), which keeps every value whose fp32 GELU is not within a few ulps of a tie bit-equal."""
+    from autokernel_amd.kernels.matmul import gemm_bias_gelu
+    for dt in (torch.float16, torch.bfloat16):
+        vals = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(dt)
+        vals = vals[torch.isfinite(vals)]
+        N = vals.numel() // 256
+        assert N * 256 == vals.numel(), (dt, vals.numel())
+        W = vals.view(N, 256).to(gpu)
+        A = torch.eye(256, dtype=dt, device=gpu)
+        out = gemm_bias_gelu(A, W.t(), torch.zeros(N, dtype=dt, device=gpu))
+        exp = torch.nn.functional.gelu(W.t().contiguous())
+        _gelu_matches_torch(out, exp, f"every {dt} value through the GELU epilogue")

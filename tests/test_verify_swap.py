@@ -245,7 +245,8 @@ def test_gpt2_and_bert_strategies_apply_and_restore():
         before = {n: type(x) for n, x in model.named_modules()}
         ctx = verify.OptimizedModelContext(model, verify.ALL_KERNELS)
         with ctx as m:
-            assert ctx.applied == {"attention": 2, "matmul": 5, "layernorm": 5}, (type(model), ctx.applied)
+            assert ctx.applied == {"attention": 2, "gelu_mlp": 2, "matmul": 1, "layernorm": 5,
+                                   "residual_block": 2}, (type(model), ctx.applied)
             assert sum(isinstance(x, attn) for x in m.modules()) == 2
         assert {n: type(x) for n, x in model.named_modules()} == before
 
@@ -266,3 +267,27 @@ def test_fused_qkv_weight_follows_weight_updates():
         assert w1 is not w0 and torch.equal(w1[att.wq.weight.shape[0]:][:att.wk.weight.shape[0]], att.wk.weight)
         att.wv.weight = torch.nn.Parameter(torch.zeros_like(att.wv.weight))   # replaced
         assert torch.count_nonzero(wrap.w_qkv[-att.wv.weight.shape[0]:]) == 0
+
+
+
+def test_gpt2_and_bert_blocks_carry_their_residuals():
+    """GPT-2's pre-norm Block and BERT's post-norm layer: with flash attention and matmul swapped, each
+    block hands its residual adds to the GEMMs that end its branches and the GELU MLPs become two
+    fused-epilogue GEMMs; without flash attention only the MLPs are fused."""
+    from autokernel_amd import bert, gpt2
+    # Linears outside the MLPs: GPT-2 c_attn + c_proj per block and lm_head; BERT four per layer and the pooler
+    for model, blocks, wrapper, linears in (
+            (gpt2.GPT2(vocab_size=64, block_size=32, n_layer=2, n_head=2, n_embd=64), "transformer.h",
+             verify.GPT2BlockWrapper, 2 * 2 + 1),
+            (bert.BertModel(vocab_size=64, hidden_size=64, num_layers=2, num_heads=2, intermediate_size=128,
+                            max_seq_len=32), "layers", verify.PostNormBlockWrapper, 4 * 2 + 1)):
+        before = {n: type(x) for n, x in model.named_modules()}
+        with verify.OptimizedModelContext(model, verify.ALL_KERNELS):
+            blk = model.get_submodule(blocks)
+            assert all(isinstance(b, wrapper) for b in blk)
+            assert all(isinstance(b.original.mlp, verify.GeluMLPWrapper) for b in blk)
+        assert {n: type(x) for n, x in model.named_modules()} == before
+        ctx = verify.OptimizedModelContext(model, ["matmul", "layernorm"])
+        with ctx:
+            assert ctx.applied == {"gelu_mlp": 2, "matmul": linears, "layernorm": 5}, ctx.applied
+        assert {n: type(x) for n, x in model.named_modules()} == before

@@ -4,7 +4,7 @@ Models: autokernel_amd.gpt2.GPT2 (models/gpt2.py:87-141: 12 x 768, 12 heads, voc
 explicit-softmax causal attention, exact GELU) on token ids [2, 1024]; autokernel_amd.bert.BertModel
 (models/bert_base.py:69-114: 12 x 768, 12 heads, intermediate 3072, non-causal SDPA) on [8, 512];
 f16, seeded N(0, 0.02) weights, ids from seed 42. The swap rules are verify.py:557-637 plus
-libak355's attention strategies. Each test asserts:
+libak355's attention, GELU-MLP and residual-block strategies. Each test asserts:
   * the swaps engage where expected (module counts);
   * the north star's check: allclose to stock at atol = rtol = 1e-2, NaN / Inf only where stock has them;
   * the swapped output is on average no farther from the same weights run in fp32 than stock f16
@@ -51,7 +51,8 @@ def test_gpt2_small_plugged_in(gpu):
     ctx = verify.OptimizedModelContext(model, verify.ALL_KERNELS)
     with torch.no_grad(), ctx as m:
         out = m(ids)
-    assert ctx.applied == {"attention": 12, "matmul": 25, "layernorm": 25}, ctx.applied
+    assert ctx.applied == {"attention": 12, "gelu_mlp": 12, "matmul": 1, "layernorm": 25,
+                           "residual_block": 12}, ctx.applied
     _report("GPT-2 all swapped", ref, out, out32)
     with torch.no_grad(), verify.OptimizedModelContext(model, ["matmul", "layernorm"]) as m:
         out_ref_set = m(ids)
@@ -70,6 +71,7 @@ def test_bert_base_plugged_in(gpu):
     ctx = verify.OptimizedModelContext(model, verify.ALL_KERNELS)
     with torch.no_grad(), ctx as m:
         out_h, out = m.encode(ids), m(ids)
-    assert ctx.applied == {"attention": 12, "matmul": 12 * 2 + 1, "layernorm": 25}, ctx.applied
+    assert ctx.applied == {"attention": 12, "gelu_mlp": 12, "matmul": 1, "layernorm": 25,
+                           "residual_block": 12}, ctx.applied
     _report("BERT all swapped, hidden states", ref_h, out_h, h32)
     _report("BERT all swapped, pooled output", ref, out, out32)
