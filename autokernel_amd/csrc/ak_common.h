@@ -214,6 +214,23 @@ inline void launch_timed(F kernel, dim3 grid, dim3 block, uint32_t shmem, hipStr
 inline bool host_aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// floor(n / d) for n, d < 2^31 as one multiply and one shift (Granlund and Montgomery, "Division
+// by invariant integers using multiplication", 1994): with s = ceil(log2 d) and
+// m = ceil(2^(31+s) / d) < 2^32, (n m) >> (31 + s) = floor(n / d), because the excess
+// n (m d - 2^(31+s)) < 2^31 d <= 2^(31+s). The host computes (m, s) once per launch; a kernel's
+// 64-bit index divisions otherwise compile to long VALU sequences per thread.
+struct FastDiv {
+  uint32_t m, s;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  return FastDiv{(uint32_t)(((1ull << (31 + s)) + d - 1) / d), s};
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) {
+  return (uint32_t)(((uint64_t)n * f.m) >> (31 + f.s));
+}
+
 }  // namespace ak
 
 // Dispatch an element-type code to a traits type: AK_DISPATCH(dtype, T, { body using T; })

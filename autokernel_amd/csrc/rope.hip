@@ -6,7 +6,7 @@
 // rnd() rounds to the element type, as each elementwise tensor op of the reference does; for
 // fp32 no fused multiply-add is formed, so every element is bit-identical to the tensor ops.
 // The fast path moves one 16-byte vector of x (4 pairs for f16 / bf16) per thread with two 8-byte
-// table slices; table rows stay hot in L2 across heads.
+// table slices; table rows stay hot in L2 across heads. Index divisions use FastDiv (32-bit).
 #include <limits.h>
 
 #include "ak_common.h"
@@ -68,6 +68,26 @@ __global__ __launch_bounds__(256) void rope_vec(const typename T::S* __restrict_
   st16(y + i * T::kVec, rope_chunk<T>(xv, ct + trow * half + c * kP, st + trow * half + c * kP));
 }
 
+// The same with 32-bit indices (chunks, rows, table entries below 2^31) and the row, column and
+// table-row divisions done by FastDiv: 6 % faster than 64-bit division at 34 MB (cold, rocprofv3).
+template <typename T>
+__global__ __launch_bounds__(256) void rope_vec32(const typename T::S* __restrict__ x,
+                                                  const typename T::S* __restrict__ ct,
+                                                  const typename T::S* __restrict__ st,
+                                                  typename T::S* __restrict__ y, uint32_t nchunks, uint32_t cpr,
+                                                  FastDiv f_cpr, uint32_t half, FastDiv f_rep, uint32_t table_rows,
+                                                  FastDiv f_tab) {
+  constexpr int kP = T::kVec / 2;
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= nchunks) return;
+  const u32x4 xv = ld16(x + (int64_t)i * T::kVec);
+  const uint32_t row = fdiv(i, f_cpr);
+  const uint32_t c = i - row * cpr;
+  const uint32_t q = fdiv(row, f_rep);
+  const uint32_t toff = (q - fdiv(q, f_tab) * table_rows) * half + c * kP;
+  st16(y + (int64_t)i * T::kVec, rope_chunk<T>(xv, ct + toff, st + toff));
+}
+
 // Any alignment: one pair per thread.
 template <typename T>
 __global__ __launch_bounds__(256) void rope_scalar(const typename T::S* __restrict__ x,
@@ -119,6 +139,36 @@ __global__ __launch_bounds__(256) void rope_f32t_vec(const typename T::S* __rest
   }
   st16(y + i * T::kVec, yv);
 }
+// rope_f32t_vec with 32-bit indices and FastDiv (chunks, rows, tokens and table entries below 2^31).
+template <typename T>
+__global__ __launch_bounds__(256) void rope_f32t_vec32(const typename T::S* __restrict__ x,
+                                                      const float* __restrict__ ct,
+                                                      const float* __restrict__ st,
+                                                      typename T::S* __restrict__ y, uint32_t nchunks,
+                                                      uint32_t cpr, FastDiv f_cpr, uint32_t half, uint32_t rep_inner,
+                                                      FastDiv f_rep, uint32_t table_rows, FastDiv f_tab,
+                                                      int64_t x_tok_stride) {
+  constexpr int kP = T::kVec / 2;
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= nchunks) return;
+  const uint32_t row = fdiv(i, f_cpr);
+  const uint32_t c = i - row * cpr;
+  const uint32_t tok = fdiv(row, f_rep);
+  const uint32_t trow = tok - fdiv(tok, f_tab) * table_rows;
+  const int64_t xoff = (int64_t)tok * x_tok_stride + (int64_t)(row - tok * rep_inner) * (2 * half) + c * T::kVec;
+  const u32x4 xv = ld16(x + xoff);
+  const float* cp = ct + trow * half + c * kP;
+  const float* sp = st + trow * half + c * kP;
+  u32x4 yv;
+#pragma unroll
+  for (int p = 0; p < kP; ++p) {
+    const float a = T::lane_elem(xv, 2 * p), b = T::lane_elem(xv, 2 * p + 1);
+    const float cc = cp[p], ss = sp[p];
+    T::set_elem(yv, 2 * p, a * cc - b * ss);
+    T::set_elem(yv, 2 * p + 1, a * ss + b * cc);
+  }
+  st16(y + (int64_t)i * T::kVec, yv);
+}
 #pragma clang fp contract(on)
 
 template <typename T>
@@ -131,8 +181,15 @@ static int launch_rope(const void* x, const void* c, const void* s, void* y, int
   if (vec) {
     const int cpr = (int)(d / T::kVec);
     const int64_t n = rows * cpr;
-    rope_vec<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>(
-        (const S*)x, (const S*)c, (const S*)s, (S*)y, n, cpr, half, table_rows, rep_inner);
+    constexpr int64_t kLim = (int64_t)1 << 31;
+    if (n < kLim && rep_inner < kLim && table_rows * half < kLim) {
+      rope_vec32<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>(
+          (const S*)x, (const S*)c, (const S*)s, (S*)y, (uint32_t)n, (uint32_t)cpr, make_fastdiv((uint32_t)cpr),
+          (uint32_t)half, make_fastdiv((uint32_t)rep_inner), (uint32_t)table_rows, make_fastdiv((uint32_t)table_rows));
+    } else {
+      rope_vec<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>(
+          (const S*)x, (const S*)c, (const S*)s, (S*)y, n, cpr, half, table_rows, rep_inner);
+    }
   } else {
     const int64_t n = rows * half;
     rope_scalar<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>((const S*)x, (const S*)c, (const S*)s,
@@ -148,9 +205,17 @@ static int launch_rope_f32t(const void* x, const float* c, const float* s, void*
   using S = typename T::S;
   const int cpr = (int)(d / T::kVec);
   const int64_t n = rows * cpr;
-  rope_f32t_vec<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>((const S*)x, c, s, (S*)y, n, cpr,
-                                                                 (int)(d / 2), table_rows, rep_inner,
-                                                                 x_tok_stride);
+  constexpr int64_t kLim = (int64_t)1 << 31;
+  if (n < kLim && rep_inner < kLim && table_rows * (d / 2) < kLim) {
+    rope_f32t_vec32<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>(
+        (const S*)x, c, s, (S*)y, (uint32_t)n, (uint32_t)cpr, make_fastdiv((uint32_t)cpr), (uint32_t)(d / 2),
+        (uint32_t)rep_inner, make_fastdiv((uint32_t)rep_inner), (uint32_t)table_rows,
+        make_fastdiv((uint32_t)table_rows), x_tok_stride);
+  } else {
+    rope_f32t_vec<T><<<(unsigned)cdiv(n, 256), 256, 0, stream>>>((const S*)x, c, s, (S*)y, n, cpr,
+                                                                   (int)(d / 2), table_rows, rep_inner,
+                                                                   x_tok_stride);
+  }
   return record_launch();
 }
 
