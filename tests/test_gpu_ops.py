@@ -344,6 +344,34 @@ def test_rope_model_layout(gpu):
     assert torch.equal(out, R.rotary_embedding_ref(x, c4, s4))
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+def test_rope_index_arithmetic(gpu, dt):
+    """The kernels find a thread's row, column and table row by multiply-shift division. Divisors
+    that are not powers of two: head_dim 96 (12 or 24 vectors per row), 37 and 127 table rows,
+    3 heads per token, many table periods, rows fewer than a wave. Bit-identical to the oracle,
+    and the fp32-table model form (q as a column slice of a fused projection) bit-identical to the
+    reference model's complex rotation in fp32."""
+    from autokernel_amd import llama
+    from autokernel_amd.kernels.rotary_embedding import apply_fp32_tables
+    g = torch.Generator().manual_seed(11)
+    cases = [((3, 5, 37, 96), (37, 48)),        # [B, H, S, D]: table row = row % 37, 15 periods
+             ((2, 37, 3, 96), (1, 37, 1, 48)),  # [B, S, H, D]: table row = (row // 3) % 37
+             ((1, 7, 127, 64), (127, 32)),
+             ((2, 1, 3, 96), (3, 48))]          # 6 rows
+    for xs, ts in cases:
+        x = torch.randn(*xs, generator=g).to(dt)
+        c, s = torch.randn(*ts, generator=g).to(dt), torch.randn(*ts, generator=g).to(dt)
+        out = kernels.get("rotary_embedding")(x.to(gpu), c.to(gpu), s.to(gpu)).cpu()
+        assert torch.equal(out, R.rotary_embedding_ref(x, c, s)), (xs, ts, dt)
+    if dt != torch.float32:
+        qkv = torch.randn(2, 37, 3 * 96 + 40, generator=g).to(dt)
+        cos, sin = llama.rope_tables(96, 41)
+        q = qkv[..., :288].view(2, 37, 3, 96)
+        exp, _ = llama.apply_rotary_emb(q, q, cos, sin)
+        out = apply_fp32_tables(qkv.to(gpu)[..., :288].view(2, 37, 3, 96), cos.to(gpu), sin.to(gpu)).cpu()
+        assert torch.equal(out, exp), (dt, (out.float() - exp.float()).abs().max().item())
+
+
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("causal", [True, False])
 def test_attention_gqa_strided(gpu, D, causal):
