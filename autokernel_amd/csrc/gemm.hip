@@ -173,7 +173,9 @@ __device__ __forceinline__ float gate_up(float g_acc, float u_acc) {
 //     of 4, so the four columns never straddle a head or the rot_cols boundary.
 // The side values (R, or the cos / sin pairs) of every fragment are loaded first, then combined
 // and stored, so their latency is paid once per tile rather than once per fragment.
-// VEC: C and R rows are 8-byte aligned, so four in-range columns move as one 8-byte access.
+// VEC: four in-range columns of C (or R) move as one 8-byte access wherever that access is 8-byte
+// aligned, checked per access: any leading dimension works, and rows whose start is not 8-byte
+// aligned (an odd ldc, e.g. a 50257-column vocabulary projection) take element accesses.
 template <typename T, int NB, int EPI, bool VEC, int FM, int FN, int MST = 16, int NST = 16>
 __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const uint16_t* __restrict__ R,
                                               int64_t ldc, int M, int N, int mb, int nb,
@@ -218,7 +220,7 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
         const uint16_t* rp = R + (int64_t)m * ldc + n;
         u32x2 r = {0u, 0u};
         if (m < M) {
-          if (VEC && n + 3 < N) {
+          if (VEC && n + 3 < N && ((uintptr_t)rp & 7u) == 0) {
             r = *reinterpret_cast<const u32x2*>(rp);
           } else {
 #pragma unroll
@@ -282,7 +284,7 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
         }
       }
       uint16_t* cp = C + (int64_t)m * ldc + n;
-      if (VEC && n + 3 < N) {
+      if (VEC && n + 3 < N && ((uintptr_t)cp & 7u) == 0) {
         u32x2 o;
         o[0] = (uint32_t)T::from_f(v[0]) | ((uint32_t)T::from_f(v[1]) << 16);
         o[1] = (uint32_t)T::from_f(v[2]) | ((uint32_t)T::from_f(v[3]) << 16);
@@ -991,8 +993,10 @@ template <typename T, int NB, int EPI>
 static int launch_gemm16(const void* A, const void* B0, const void* B1, void* C, int64_t M,
                          int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, bool bt,
                          hipStream_t s, const EpiArgs& ep = EpiArgs{}) {
-  bool vec = K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && host_aligned16(A) &&
-             host_aligned16(B0) && (!B1 || EPI == kEpiBias || EPI == kEpiBiasGelu || host_aligned16(B1)) && (((uintptr_t)C) & 7u) == 0;
+  // vec: A and B load as 16-byte k-chunks (C's alignment does not matter: the epilogue checks each
+  // 8-byte store)
+  bool vec = K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && host_aligned16(A) && host_aligned16(B0) &&
+             (!B1 || EPI == kEpiBias || EPI == kEpiBiasGelu || host_aligned16(B1));
   if (!bt) vec = vec && N % 8 == 0;
   const int m = (int)M, n = (int)N, k = (int)K;
   // LDS-DMA path: nn.Linear-layout B, K a multiple of 64, 32-bit element offsets
