@@ -119,7 +119,15 @@ def require_gpu(op: str, *tensors: torch.Tensor) -> None:
                                "(autokernel_amd has no CPU path)")
 
 
+# The raw handle of a device's current stream: the value of torch.cuda.current_stream(d).cuda_stream
+# without building a Stream object (1.8 us per call -> 0.07 us; torch's compiled kernels launch the
+# same way)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

@@ -1,16 +1,7 @@
-"""Helpers shared by the kernel_fn modules: device guard, GPU check and row flattening."""
+"""Helpers shared by the kernel_fn modules: GPU check and row flattening."""
 from __future__ import annotations
 
-import contextlib
-
 import torch
-
-
-def device_guard(t: torch.Tensor):
-    """Make t's device current for the launch when it is not already."""
-    if t.device.index is not None and t.device.index != torch.cuda.current_device():
-        return torch.cuda.device(t.device)
-    return contextlib.nullcontext()
 
 
 def rows_view(x: torch.Tensor) -> torch.Tensor:

@@ -4,8 +4,8 @@ Each function has the name and signature of the torch op that the HuggingFace Ke
 registers for the same C entry point (hf_export/torch_binding.cpp): outputs first, then inputs,
 then scalars. So kernels/host.py, the one shape / dtype layer of every kernel_fn, runs unchanged
 on either: bound to this module in-tree, bound to the package's torch ops in the export. Each op
-makes the input's device current, launches on torch's current stream of that device and raises
-AkError on a non-OK status.
+makes the input's device current (when it is not already), launches on torch's current stream of
+that device and raises AkError on a non-OK status.
 """
 from __future__ import annotations
 
@@ -14,7 +14,6 @@ import functools
 import torch
 
 from .. import _lib
-from ._common import device_guard
 
 
 def _code(t: torch.Tensor, op: str) -> int:
@@ -22,11 +21,17 @@ def _code(t: torch.Tensor, op: str) -> int:
 
 
 def _run(fn_name: str, ref: torch.Tensor, *args, **info) -> None:
-    if not ref.is_cuda:
+    idx = ref.get_device()
+    if idx < 0:
         raise RuntimeError(f"{fn_name}: expected GPU tensors, got one on {ref.device} (no CPU path)")
-    with device_guard(ref):
-        st = getattr(_lib.load(), fn_name)(*args, _lib.stream_of(ref))
-    _lib.check(st, fn_name, **info)
+    fn = getattr(_lib.load(), fn_name)
+    if idx == torch.cuda.current_device():
+        st = fn(*args, _lib.stream_of(ref))
+    else:
+        with torch.cuda.device(idx):
+            st = fn(*args, _lib.stream_of(ref))
+    if st != _lib.AK_OK:
+        _lib.check(st, fn_name, **info)
 
 
 def rmsnorm(y: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: float) -> None:

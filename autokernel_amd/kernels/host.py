@@ -38,6 +38,8 @@ def _check(op: str, *ts) -> None:
 
 def _rows(x: torch.Tensor) -> torch.Tensor:
     """[..., N] -> contiguous [rows, N]."""
+    if x.dim() == 2 and x.is_contiguous():
+        return x  # the common case, without the cost of two more torch calls
     if x.dim() == 0:
         x = x.reshape(1, 1)
     elif x.dim() == 1:
@@ -50,31 +52,40 @@ def _as(t, dtype):
     return t if t is None or t.dtype == dtype else t.to(dtype)
 
 
+def _vec(t):
+    """A weight / bias as a contiguous 1-D tensor (itself when it already is one)."""
+    if t is None or (t.dim() == 1 and t.is_contiguous()):
+        return t
+    return t.contiguous().view(-1)
+
+
+def _shaped(y: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    return y if y.dim() == x.dim() else y.view(x.shape)
+
+
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     _check("rmsnorm", x, weight)
     x2 = _rows(x)
-    w = _as(weight, x.dtype).contiguous().view(-1)
+    w = _vec(_as(weight, x.dtype))
     if w.numel() != x2.shape[1]:
         raise ValueError(f"rmsnorm: weight has {w.numel()} elements, x rows have {x2.shape[1]}")
     y = torch.empty_like(x2)
     ops.rmsnorm(y, x2, w, float(eps))
-    return y.view(x.shape)
+    return _shaped(y, x)
 
 
 def layernorm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor | None,
               eps: float = 1e-5) -> torch.Tensor:
     _check("layernorm", x, weight, bias)
     x2 = _rows(x)
-    w = _as(weight, x.dtype)
-    b = _as(bias, x.dtype)
-    w = None if w is None else w.contiguous().view(-1)
-    b = None if b is None else b.contiguous().view(-1)
+    w = _vec(_as(weight, x.dtype))
+    b = _vec(_as(bias, x.dtype))
     for name, t in (("weight", w), ("bias", b)):
         if t is not None and t.numel() != x2.shape[1]:
             raise ValueError(f"layernorm: {name} has {t.numel()} elements, x rows have {x2.shape[1]}")
     y = torch.empty_like(x2)
     ops.layernorm(y, x2, w, b, float(eps))
-    return y.view(x.shape)
+    return _shaped(y, x)
 
 
 def softmax(x: torch.Tensor, dim: int = -1) -> torch.Tensor:
