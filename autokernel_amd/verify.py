@@ -468,6 +468,26 @@ class EncoderAttentionWrapper(nn.Module):
         super().__init__()
         self.original = original
         self.use_matmul = use_matmul
+        # query / key / value as one GEMM over a concatenated [3C, C] weight (and bias): q, k and v
+        # are column slices of its output, read in place by the attention kernel. Each output
+        # element is the same dot product in the same order as in three separate GEMMs. The copy
+        # is rebuilt whenever a source weight or bias changes (tracked by version and storage).
+        lins = (original.query, original.key, original.value)
+        self.fused_qkv = use_matmul and len({l.bias is None for l in lins}) == 1
+        self._qkv_key = None
+        self._w_qkv = self._b_qkv = None
+
+    def _qkv_params(self):
+        o = self.original
+        ps = [t for l in (o.query, o.key, o.value) for t in (l.weight, l.bias) if t is not None]
+        key = tuple((t.data_ptr(), t._version, t.dtype, tuple(t.shape)) for t in ps)
+        if key != self._qkv_key:
+            with torch.no_grad():
+                self._w_qkv = torch.cat([o.query.weight, o.key.weight, o.value.weight], 0).contiguous()
+                self._b_qkv = None if o.query.bias is None else torch.cat(
+                    [o.query.bias, o.key.bias, o.value.bias], 0).contiguous()
+            self._qkv_key = key
+        return self._w_qkv, self._b_qkv
 
     def forward(self, x, attention_mask=None, residual: Optional[torch.Tensor] = None):
         o = self.original
@@ -480,7 +500,11 @@ class EncoderAttentionWrapper(nn.Module):
 
         def proj(lin, t):
             return _linear(t, lin.weight, lin.bias) if self.use_matmul else lin(t)
-        q, k, v = (proj(lin, x).view(B, T, H, D) for lin in (o.query, o.key, o.value))
+        if self.fused_qkv:
+            qkv = _linear(x, *self._qkv_params())
+            q, k, v = (qkv[..., i * C:(i + 1) * C].view(B, T, H, D) for i in range(3))
+        else:
+            q, k, v = (proj(lin, x).view(B, T, H, D) for lin in (o.query, o.key, o.value))
         y = torch.empty((B, T, H, D), device=x.device, dtype=x.dtype)  # written in place, no transpose copy
         fa_mod.attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), False, None, out=y.transpose(1, 2))
         y = y.view(B, T, C)
