@@ -269,6 +269,29 @@ def test_fused_qkv_weight_follows_weight_updates():
         assert torch.count_nonzero(wrap.w_qkv[-att.wv.weight.shape[0]:]) == 0
 
 
+def test_encoder_fused_qkv_follows_parameter_updates():
+    """BERT-style attention's concatenated [query; key; value] weight and bias are rebuilt when a
+    source weight or bias changes in place or is replaced, and reused otherwise."""
+    import torch
+    from autokernel_amd import bert
+    model = bert.BertModel(vocab_size=64, hidden_size=64, num_layers=1, num_heads=2, intermediate_size=128,
+                           max_seq_len=32)
+    with verify.OptimizedModelContext(model, verify.ALL_KERNELS) as m:
+        wrap = next(x for x in m.modules() if isinstance(x, verify.EncoderAttentionWrapper))
+        att = wrap.original
+        assert wrap.fused_qkv
+        w0, b0 = wrap._qkv_params()
+        assert torch.equal(w0, torch.cat([att.query.weight, att.key.weight, att.value.weight]))
+        assert torch.equal(b0, torch.cat([att.query.bias, att.key.bias, att.value.bias]))
+        assert wrap._qkv_params()[0] is w0                 # unchanged parameters: no rebuild
+        with torch.no_grad():
+            att.key.bias.add_(1.0)                         # in-place update of a bias
+        w1, b1 = wrap._qkv_params()
+        assert w1 is not w0 and torch.equal(b1[64:128], att.key.bias)
+        att.value.weight = torch.nn.Parameter(torch.zeros_like(att.value.weight))   # replaced
+        assert torch.count_nonzero(wrap._qkv_params()[0][128:]) == 0
+
+
 
 def test_gpt2_and_bert_blocks_carry_their_residuals():
     """GPT-2's pre-norm Block and BERT's post-norm layer: with flash attention and matmul swapped, each
