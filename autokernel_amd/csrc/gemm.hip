@@ -850,17 +850,22 @@ struct TileCfg {
 // Pick the tile that keeps the 256 CUs busiest: fraction of CU-slots doing useful work over the
 // launch, weighted by the per-tile efficiency of smaller tiles (more LDS and L2 traffic per flop).
 // wide192: also consider 256x192 tiles (the LDS-DMA kernel with nn.Linear-layout B; 2048 x 6144,
-// a fused QKV projection, is then exactly one tile per CU)
-static TileCfg pick_tile(int64_t M, int64_t N, int nb, bool wide192 = false) {
-  const TileCfg cands[] = {{256, 256}, {256, 128}, {128, 128}, {256, 192}};
+// a fused QKV projection, is then exactly one tile per CU). small64: also consider 64x64 tiles
+// (the same kernel and layout, for grids that 128x128 tiles leave mostly idle; the [K, N]-B
+// layout's LDS swizzle needs rows of at least 128 elements).
+static TileCfg pick_tile(int64_t M, int64_t N, int nb, bool wide192 = false, bool small64 = false) {
+  const TileCfg cands[] = {{256, 256}, {256, 128}, {128, 128}, {256, 192}, {64, 64}};
   // relative per-flop throughput of the tiles (bf16, MI355X): 4096^3 on 256x256 1230 TF/s,
-  // 2048x4096x4096 on 256x128 1084 TF/s, 2048x6144x4096 on 128x128 786 TF/s, on 256x192 1108 TF/s
-  const double eff[] = {1.0, 0.88, 0.64, 0.88};
+  // 2048x4096x4096 on 256x128 1084 TF/s, 2048x6144x4096 on 128x128 786 TF/s, on 256x192 1108 TF/s;
+  // 64x64 weighted so that it wins only where 128x128 tiles fill under a third of the CUs (cold,
+  // f16: 2048x768x768 16.4 -> 13.8 us, 2048x768x3072 41.7 -> 37.3 us, 4096x768x768 unchanged
+  // at 15.1 us; with a weight of 0.5 it was also picked there and took 16.3 us)
+  const double eff[] = {1.0, 0.88, 0.64, 0.88, 0.35};
   const int cus = 256;
   TileCfg best = cands[2];
   double best_s = -1.0;
-  const int ncand = (wide192 && nb == 1) ? 4 : 3;
-  for (int i = 0; i < ncand; ++i) {
+  for (int i = 0; i < 5; ++i) {
+    if ((i == 3 && !(wide192 && nb == 1)) || (i == 4 && !(small64 && nb == 1))) continue;
     const int bn = cands[i].bn / (nb == 2 ? 2 : 1);
     const int64_t tiles = cdiv(M, cands[i].bm) * cdiv(N, bn);
     const int64_t waves = cdiv(tiles, cus);
@@ -968,11 +973,17 @@ template <typename T, int NB, int EPI, bool BKN>
 static void launch_gemm_dma(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
                             int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s, const EpiArgs& ep) {
   // 256x192 needs [N, K] B: a [K, N] B tile row of 192 elements does not split into 1 KB transfers
-  const TileCfg t = pick_tile(M, N, NB, !BKN);
+  const TileCfg t = pick_tile(M, N, NB, !BKN, !BKN && EPI != kEpiPartial);
   if constexpr (NB == 1) {
     if constexpr (!BKN) {
       if (t.bm == 256 && t.bn == 192) {
         launch_dma_cfg<T, 256, 192, 2, 4, 1, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
+        return;
+      }
+    }
+    if constexpr (!BKN) {
+      if (t.bm == 64) {
+        launch_dma_cfg<T, 64, 64, 2, 2, 1, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
         return;
       }
     }

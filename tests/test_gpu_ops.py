@@ -606,11 +606,17 @@ def _rand_shapes(seed, n, lo, hi, align_choices):
     return out
 
 
-@pytest.mark.parametrize("M,N,K", _rand_shapes(7, 10, 1, 700, (1, 4, 1)) + _rand_shapes(8, 6, 64, 1600, (16, 8, 64)))
+# grids that 128x128 tiles would leave mostly idle: the nn.Linear-layout B takes 64x64 tiles there
+SMALL_GRID_SHAPES = [(2048, 768, 768), (2048, 768, 3072), (1024, 1024, 1024), (65, 130, 192), (64, 64, 64)]
+
+
+@pytest.mark.parametrize("M,N,K", _rand_shapes(7, 10, 1, 700, (1, 4, 1)) + _rand_shapes(8, 6, 64, 1600, (16, 8, 64))
+                         + SMALL_GRID_SHAPES)
 def test_gemm_epilogues_random_shapes(gpu, M, N, K):
-    """Seeded random shapes across the LDS-DMA path (K % 64 == 0), the register-staged fallback
-    and ragged tile edges: plain, residual and rotary epilogues in f16 and bf16, both B layouts;
-    the epilogue variants equal the plain GEMM followed by the separate op, bit for bit."""
+    """Seeded random shapes across the LDS-DMA path (K % 64 == 0, 64x64 to 256x256 tiles), the
+    register-staged fallback and ragged tile edges, plus shapes whose grids take the small tiles:
+    plain, residual and rotary epilogues in f16 and bf16, both B layouts; the epilogue variants
+    equal the plain GEMM followed by the separate op, bit for bit."""
     from autokernel_amd import llama
     from autokernel_amd.kernels.matmul import gemm, gemm_residual, gemm_rope
     g = torch.Generator().manual_seed(M * 1009 + N * 31 + K)
@@ -710,7 +716,8 @@ def test_gemm_padded_kn_view_not_split(gpu, N):
     assert_close(out[:, -4:], exp[:, -4:], 1e-2, 1e-2, "last four columns")
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 2304, 768), (300, 520, 200), (8 * 512, 3072, 768), (64, 50257, 768)])
+@pytest.mark.parametrize("M,N,K", [(2048, 2304, 768), (300, 520, 200), (8 * 512, 3072, 768), (64, 50257, 768),
+                                   (2048, 768, 768)])
 def test_gemm_bias_one_rounding(gpu, M, N, K):
     """ak_gemm_bias: x @ W.T + bias with the bias added to the fp32 accumulator and one rounding,
     against the oracle's fp32 product + bias rounded once (f16 and bf16, nn.Linear layout), and
@@ -752,7 +759,8 @@ def _gelu_matches_torch(out: torch.Tensor, exp: torch.Tensor, what: str) -> None
     assert n_diff <= max(4, out.numel() // 100000), what
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 3072, 768), (8 * 512, 768, 3072), (300, 520, 200), (257, 77, 96)])
+@pytest.mark.parametrize("M,N,K", [(2048, 3072, 768), (8 * 512, 768, 3072), (300, 520, 200), (257, 77, 96),
+                                   (2048, 768, 3072)])
 def test_gemm_bias_gelu_and_residual_epilogues(gpu, M, N, K):
     """ak_gemm_bias_gelu and ak_gemm_bias_residual (GPT-2 / BERT MLP and output-projection shapes, an
     unaligned N that takes the register-staged path), f16 and bf16: ak_gemm_bias followed by torch's
