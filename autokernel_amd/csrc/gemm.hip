@@ -507,10 +507,18 @@ struct DmaGeom<32> {
 // 8 consecutive k of one n per lane: two ds_read_b64_tr_b16 each give 4. That instruction
 // transposes across each group of 16 lanes: output lane i, element e = element (i % 4) of source
 // lane (i / 4 + 4 e); so source lane j addresses B[k0 + j / 4][n0 + 4 (j % 4)] and output lane i
-// receives B[k0 + e][n0 + i]. 16-byte chunk c of tile row k is stored at c ^ bkn_swz(k): the 16
+// receives B[k0 + e][n0 + i]. 16-byte chunk c of tile row k is stored at c ^ bkn_swz<BN>(k): the 16
 // rows of one tr read (4 per lane group) land on distinct banks for lane groups {0,1}, {2,3},
 // {0,2} and {1,3}.
-__device__ __forceinline__ int bkn_swz(int k) { return 2 * ((k & 3) + 4 * (((k >> 3) ^ (k >> 4)) & 1)); }
+// A 64-element tile row (BN = 64) has 8 chunks and 128 bytes, so rows r and r + 2 share banks: the
+// pattern 2 ((k >> 1) & 1) + 4 (((k >> 3) ^ (k >> 4)) & 1) keeps each read's chunk pair inside the row
+// and gives rows {0, 2, 8, 10}, {0, 2, 16, 18} and {8, 10, 24, 26} distinct chunk pairs (rows + 4,
+// the second read, share the pattern).
+template <int BN>
+__device__ __forceinline__ int bkn_swz(int k) {
+  if constexpr (BN == 64) return 2 * (((k >> 1) & 1) + 2 * (((k >> 3) ^ (k >> 4)) & 1));
+  else return 2 * ((k & 3) + 4 * (((k >> 3) ^ (k >> 4)) & 1));
+}
 
 typedef short gemm_s16x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u32x2 lds_tr16(const uint16_t* p) {
@@ -578,7 +586,7 @@ __device__ __forceinline__ void gemm_dma_ns_kloop(
           const uint16_t* bs = sp + (BM + b * BN) * BKD;
           const int row = s * 32 + 8 * fc + (fr >> 2);
           const int col = wn * WTN + j * 16 + 4 * (fr & 3);
-          const uint16_t* p = bs + row * BN + (((col >> 3) ^ bkn_swz(row)) * 8) + (col & 7);
+          const uint16_t* p = bs + row * BN + (((col >> 3) ^ bkn_swz<BN>(row)) * 8) + (col & 7);
           const u32x2 lo = lds_tr16(p);
           const u32x2 hi = lds_tr16(p + 4 * BN);  // rows + 4 share the swizzle
           dst[b][j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
@@ -693,7 +701,7 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
       // clamped onto the last full chunk (their results are never stored)
       constexpr int CPR = BN / 8;
       const int row = (i * NW + wid) * GB::RPI + lane / CPR;
-      const int lc = (lane % CPR) ^ bkn_swz(row);
+      const int lc = (lane % CPR) ^ bkn_swz<BN>(row);
       ob[i] = 2u * (uint32_t)(row * (int)ldb + min(n0 + lc * 8, N - 8));
     } else {
       const int row = (i * NW + wid) * RPI + r_in;
@@ -851,15 +859,15 @@ struct TileCfg {
 // launch, weighted by the per-tile efficiency of smaller tiles (more LDS and L2 traffic per flop).
 // wide192: also consider 256x192 tiles (the LDS-DMA kernel with nn.Linear-layout B; 2048 x 6144,
 // a fused QKV projection, is then exactly one tile per CU). small64: also consider 64x64 tiles
-// (the same kernel and layout, for grids that 128x128 tiles leave mostly idle; the [K, N]-B
-// layout's LDS swizzle needs rows of at least 128 elements).
+// (the same kernel, for grids that 128x128 tiles leave mostly idle).
 static TileCfg pick_tile(int64_t M, int64_t N, int nb, bool wide192 = false, bool small64 = false) {
   const TileCfg cands[] = {{256, 256}, {256, 128}, {128, 128}, {256, 192}, {64, 64}};
   // relative per-flop throughput of the tiles (bf16, MI355X): 4096^3 on 256x256 1230 TF/s,
   // 2048x4096x4096 on 256x128 1084 TF/s, 2048x6144x4096 on 128x128 786 TF/s, on 256x192 1108 TF/s;
   // 64x64 weighted so that it wins only where 128x128 tiles fill under a third of the CUs (cold,
-  // f16: 2048x768x768 16.4 -> 13.8 us, 2048x768x3072 41.7 -> 37.3 us, 4096x768x768 unchanged
-  // at 15.1 us; with a weight of 0.5 it was also picked there and took 16.3 us)
+  // f16: 2048x768x768 16.4 -> 13.8 us, 2048x768x3072 41.7 -> 37.3 us, 1024^3 NN 17.3 -> 15.5 us,
+  // 4096x768x768 unchanged at 15.1 us; with a weight of 0.5 it was also picked there and took
+  // 16.3 us)
   const double eff[] = {1.0, 0.88, 0.64, 0.88, 0.35};
   const int cus = 256;
   TileCfg best = cands[2];
@@ -973,7 +981,7 @@ template <typename T, int NB, int EPI, bool BKN>
 static void launch_gemm_dma(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
                             int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s, const EpiArgs& ep) {
   // 256x192 needs [N, K] B: a [K, N] B tile row of 192 elements does not split into 1 KB transfers
-  const TileCfg t = pick_tile(M, N, NB, !BKN, !BKN && EPI != kEpiPartial);
+  const TileCfg t = pick_tile(M, N, NB, !BKN, EPI != kEpiPartial);
   if constexpr (NB == 1) {
     if constexpr (!BKN) {
       if (t.bm == 256 && t.bn == 192) {
@@ -981,11 +989,9 @@ static void launch_gemm_dma(const void* A, const void* B0, const void* B1, void*
         return;
       }
     }
-    if constexpr (!BKN) {
-      if (t.bm == 64) {
-        launch_dma_cfg<T, 64, 64, 2, 2, 1, EPI, false>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
-        return;
-      }
+    if (t.bm == 64) {
+      launch_dma_cfg<T, 64, 64, 2, 2, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
+      return;
     }
     if (t.bm == 256 && t.bn == 256)
       launch_dma_cfg<T, 256, 256, 2, kBigWN, 1, EPI, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
