@@ -42,6 +42,7 @@ SIGNATURES: dict[str, list] = {
     "ak_reduce_sum": [_i, _p, _p, _i64, _i64, _i64, _p],
     "ak_reduce_max": [_i, _p, _p, _i64, _i64, _i64, _p],
     "ak_gemm": [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],
+    "ak_gemm_batched": [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],
     "ak_gemm_residual": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],
     "ak_gemm_bias": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],
     "ak_gemm_bias_gelu": [_i, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p],

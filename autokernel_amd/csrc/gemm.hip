@@ -127,7 +127,23 @@ struct EpiArgs {
   int seq_len = 1;
   int splits = 1;
   int64_t split_a = 0, split_b = 0, split_c = 0;
+  // Batched products (ak_gemm_batched): grid z is the batch item; item z reads A and B advanced by
+  // z * batch_a / z * batch_b elements and writes C advanced by z * batch_c (a stride of 0 shares
+  // the operand across the batch).
+  int batch = 1;
+  int64_t batch_a = 0, batch_b = 0, batch_c = 0;
 };
+
+// Bases of this block's batch item (grid z); one item when ep.batch == 1.
+template <class PA, class PB, class PC>
+__device__ __forceinline__ void batch_bases(PA& A, PB& B, PC& C, const EpiArgs& ep) {
+  if (ep.batch > 1) {
+    const int64_t z = blockIdx.z;
+    A += z * ep.batch_a;
+    B += z * ep.batch_b;
+    C += z * ep.batch_c;
+  }
+}
 
 // The model's rotation of one pair in fp32, each product and sum rounded on its own (no fused
 // multiply-add), as separate fp32 tensor ops compute (a c - b s, a s + b c).
@@ -317,6 +333,7 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma(
 
   __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * kBK];
   __shared__ __attribute__((aligned(16))) uint16_t sB[2][NB][BN * kBK];
+  batch_bases(A, B0, C, ep);
 
   int tm, tn;
   tile_coords(tiles_m, tiles_n, &tm, &tn);
@@ -675,6 +692,7 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_dma(
     B0 += z * ep.split_b;
     C += 2 * z * ep.split_c;  // fp32 workspace addressed in 16-bit units
   }
+  batch_bases(A, B0, C, ep);
   int tm, tn;
   tile_coords(tiles_m, tiles_n, &tm, &tn);
   const int m0 = tm * BM, n0 = tn * BN;
@@ -860,7 +878,8 @@ struct TileCfg {
 // wide192: also consider 256x192 tiles (the LDS-DMA kernel with nn.Linear-layout B; 2048 x 6144,
 // a fused QKV projection, is then exactly one tile per CU). small64: also consider 64x64 tiles
 // (the same kernel, for grids that 128x128 tiles leave mostly idle).
-static TileCfg pick_tile(int64_t M, int64_t N, int nb, bool wide192 = false, bool small64 = false) {
+static TileCfg pick_tile(int64_t M, int64_t N, int nb, bool wide192 = false, bool small64 = false,
+                         int64_t batch = 1) {
   const TileCfg cands[] = {{256, 256}, {256, 128}, {128, 128}, {256, 192}, {64, 64}};
   // relative per-flop throughput of the tiles (bf16, MI355X): 4096^3 on 256x256 1230 TF/s,
   // 2048x4096x4096 on 256x128 1084 TF/s, 2048x6144x4096 on 128x128 786 TF/s, on 256x192 1108 TF/s;
@@ -875,7 +894,7 @@ static TileCfg pick_tile(int64_t M, int64_t N, int nb, bool wide192 = false, boo
   for (int i = 0; i < 5; ++i) {
     if ((i == 3 && !(wide192 && nb == 1)) || (i == 4 && !(small64 && nb == 1))) continue;
     const int bn = cands[i].bn / (nb == 2 ? 2 : 1);
-    const int64_t tiles = cdiv(M, cands[i].bm) * cdiv(N, bn);
+    const int64_t tiles = cdiv(M, cands[i].bm) * cdiv(N, bn) * batch;
     const int64_t waves = cdiv(tiles, cus);
     const double used = (double)tiles / (double)(waves * cus);
     // padding waste inside edge tiles
@@ -893,7 +912,7 @@ template <typename T, bool BT, bool VEC, int BM, int BN, int WM, int WN, int NB,
 static void launch_gemm_cfg(const void* A, const void* B0, const void* B1, void* C, int M, int N,
                             int K, int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s, const EpiArgs& ep) {
   const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(N, BN);
-  gemm_mfma<T, BT, VEC, BM, BN, WM, WN, NB, EPI><<<tiles_m * tiles_n, WM * WN * kWave, 0, s>>>(
+  gemm_mfma<T, BT, VEC, BM, BN, WM, WN, NB, EPI><<<dim3(tiles_m * tiles_n, 1, ep.batch), WM * WN * kWave, 0, s>>>(
       (const uint16_t*)A, (const uint16_t*)B0, (const uint16_t*)B1, (uint16_t*)C, M, N, K, lda, ldb,
       ldc, tiles_m, tiles_n, ep);
 }
@@ -905,7 +924,7 @@ constexpr int kBigWN = 4;
 template <typename T, bool BT, bool VEC, int NB, int EPI>
 static void launch_gemm_tiled(const void* A, const void* B0, const void* B1, void* C, int M, int N,
                               int K, int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s, const EpiArgs& ep) {
-  const TileCfg t = pick_tile(M, N, NB);
+  const TileCfg t = pick_tile(M, N, NB, false, false, ep.batch);
   if constexpr (NB == 1) {
     if (t.bm == 256 && t.bn == 256)
       launch_gemm_cfg<T, BT, VEC, 256, 256, 2, kBigWN, 1, EPI>(A, B0, B1, C, M, N, K, lda, ldb, ldc, s, ep);
@@ -931,7 +950,7 @@ static void launch_dma_kernel(const void* A, const void* B0, const void* B1, voi
                               const EpiArgs& ep) {
   // MFMA shape 16x16x32 (32x32x16 fragments measured 4-10 % slower on every workload)
   constexpr int MF = 16;
-  gemm_dma<T, BM, BN, WM, WN, NB, EPI, BKD, NS, BKN, MF><<<dim3(tiles_m * tiles_n, ep.splits), WM * WN * kWave, 0, s>>>(
+  gemm_dma<T, BM, BN, WM, WN, NB, EPI, BKD, NS, BKN, MF><<<dim3(tiles_m * tiles_n, ep.splits, ep.batch), WM * WN * kWave, 0, s>>>(
       (const uint16_t*)A, (const uint16_t*)B0, (const uint16_t*)B1, (uint16_t*)C, M, N, K, lda, ldb, ldc,
       tiles_m, tiles_n, ep);
 }
@@ -967,7 +986,7 @@ static void launch_dma_cfg(const void* A, const void* B0, const void* B1, void* 
   // 64-deep pair is faster per tile (2048x6144x4096 on 192 tiles of 256x256: 109.9 us against
   // 127.5 us).
   constexpr bool kOk32 = P::kOk32;
-  if (kOk32 && 2 * tiles_m * tiles_n * ep.splits <= kCUs) {
+  if (kOk32 && 2 * tiles_m * tiles_n * ep.splits * ep.batch <= kCUs) {
     if constexpr (kOk32)
       launch_dma_kernel<T, BM, BN, WM, WN, NB, EPI, 32, 4, BKN>(A, B0, B1, C, M, N, K, lda, ldb, ldc, tiles_m,
                                                                 tiles_n, s, ep);
@@ -981,7 +1000,7 @@ template <typename T, int NB, int EPI, bool BKN>
 static void launch_gemm_dma(const void* A, const void* B0, const void* B1, void* C, int M, int N, int K,
                             int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s, const EpiArgs& ep) {
   // 256x192 needs [N, K] B: a [K, N] B tile row of 192 elements does not split into 1 KB transfers
-  const TileCfg t = pick_tile(M, N, NB, !BKN, EPI != kEpiPartial);
+  const TileCfg t = pick_tile(M, N, NB, !BKN, EPI != kEpiPartial, ep.batch);
   if constexpr (NB == 1) {
     if constexpr (!BKN) {
       if (t.bm == 256 && t.bn == 192) {
@@ -1013,7 +1032,8 @@ static int launch_gemm16(const void* A, const void* B0, const void* B1, void* C,
   // vec: A and B load as 16-byte k-chunks (C's alignment does not matter: the epilogue checks each
   // 8-byte store)
   bool vec = K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && host_aligned16(A) && host_aligned16(B0) &&
-             (!B1 || EPI == kEpiBias || EPI == kEpiBiasGelu || host_aligned16(B1));
+             (!B1 || EPI == kEpiBias || EPI == kEpiBiasGelu || host_aligned16(B1)) && ep.batch_a % 8 == 0 &&
+             ep.batch_b % 8 == 0;
   if (!bt) vec = vec && N % 8 == 0;
   const int m = (int)M, n = (int)N, k = (int)K;
   // LDS-DMA path: nn.Linear-layout B, K a multiple of 64, 32-bit element offsets
@@ -1228,6 +1248,45 @@ extern "C" int ak_gemm(int dtype, const void* A, const void* B, void* C, int64_t
     case AK_BF16: return launch_gemm16<TBF16, 1, kEpiStore>(A, B, nullptr, C, M, N, K, lda, ldb, ldc, bt, stream);
     default: return AK_EINVAL;
   }
+}
+
+extern "C" int ak_gemm_batched(int dtype, const void* A, const void* B, void* C, int64_t batch, int64_t M,
+                               int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t stride_a,
+                               int64_t stride_b, int64_t stride_c, int b_trans, hipStream_t stream) {
+  if (batch < 0 || M < 0 || N < 0 || K < 0 || M > INT_MAX || N > INT_MAX || K > INT_MAX) return AK_EINVAL;
+  if (batch == 0 || M == 0 || N == 0) return AK_OK;
+  if (!A || !B || !C) return AK_EINVAL;
+  if (lda < K || ldc < N || ldb < (b_trans ? K : N) || stride_a < 0 || stride_b < 0) return AK_EINVAL;
+  // the batch items of C must not overlap (each is written once, in parallel)
+  if (batch > 1 && stride_c < (M - 1) * ldc + N) return AK_EINVAL;
+  if (cdiv(M, 128) * cdiv(N, 128) > INT_MAX) return AK_EINVAL;
+  const bool bt = b_trans != 0;
+  const int esz = dtype == AK_F32 ? 4 : 2;
+  // grid z holds at most 65535 items: larger batches run in chunks
+  constexpr int64_t kMaxZ = 65535;
+  for (int64_t z0 = 0; z0 < batch; z0 += kMaxZ) {
+    const int64_t nz = batch - z0 < kMaxZ ? batch - z0 : kMaxZ;
+    const char* a = (const char*)A + z0 * stride_a * esz;
+    const char* b = (const char*)B + z0 * stride_b * esz;
+    char* c = (char*)C + z0 * stride_c * esz;
+    int st = AK_OK;
+    if (dtype == AK_F32) {
+      for (int64_t z = 0; z < nz && st == AK_OK; ++z)
+        st = launch_gemm32(a + z * stride_a * 4, b + z * stride_b * 4, c + z * stride_c * 4, M, N, K, lda, ldb,
+                           ldc, bt, stream);
+    } else {
+      EpiArgs ep;
+      ep.batch = (int)nz;
+      ep.batch_a = stride_a;
+      ep.batch_b = stride_b;
+      ep.batch_c = stride_c;
+      if (dtype == AK_F16) st = launch_gemm16<TF16, 1, kEpiStore>(a, b, nullptr, c, M, N, K, lda, ldb, ldc, bt, stream, ep);
+      else if (dtype == AK_BF16) st = launch_gemm16<TBF16, 1, kEpiStore>(a, b, nullptr, c, M, N, K, lda, ldb, ldc, bt, stream, ep);
+      else return AK_EINVAL;
+    }
+    if (st != AK_OK) return st;
+  }
+  return AK_OK;
 }
 
 extern "C" int64_t ak_gemm_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,

@@ -57,7 +57,7 @@ OP_BINDINGS = {
     "rotary_embedding": ("rope",),
     "cross_entropy": ("cross_entropy",),
     "reduce": ("reduce_sum", "reduce_max"),
-    "matmul": ("gemm", "gemm_workspace_bytes"),
+    "matmul": ("gemm", "gemm_batched", "gemm_workspace_bytes"),
     "fused_mlp": ("mlp_gate_up", "gemm"),
     "flash_attention": ("flash_attn_fwd",),
 }

@@ -222,6 +222,31 @@ void ak_op_gemm(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, bool b_
                "ak_gemm");
 }
 
+// c [Z, M, N] = a [Z, M, K] @ op(b) per batch item (torch.matmul's batched product): b is stored
+// [Z, K, N] (b_trans false) or [Z, N, K] (true). Unit stride along each last dim; row and batch
+// strides are passed (a batch stride of 0 shares an operand across the batch).
+void ak_op_gemm_batched(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, bool b_trans) {
+  const char* op = "matmul";
+  on_gpu(a, a, op, "a");
+  on_gpu(b, a, op, "b");
+  on_gpu(c, a, op, "c");
+  TORCH_CHECK(a.dim() == 3 && b.dim() == 3 && c.dim() == 3, op, ": batched a, b, c must be 3-D");
+  const int64_t Z = a.size(0), M = a.size(1), K = a.size(2);
+  const int64_t N = b_trans ? b.size(1) : b.size(2);
+  TORCH_CHECK(b.size(0) == Z && (b_trans ? b.size(2) : b.size(1)) == K, op, ": shapes ", a.sizes(), " and ",
+              b.sizes(), (b_trans ? " (transposed)" : ""), " do not align");
+  TORCH_CHECK(c.size(0) == Z && c.size(1) == M && c.size(2) == N, op, ": c shape ", c.sizes(), " != [", Z, ", ",
+              M, ", ", N, "]");
+  const at::Tensor* operands[] = {&a, &b, &c};
+  for (const at::Tensor* t : operands)
+    TORCH_CHECK(t->size(2) <= 1 || t->stride(2) == 1, op, ": operands need a unit stride along their last dim");
+  auto ld = [](const at::Tensor& t) { return t.size(1) > 1 ? t.stride(1) : std::max<int64_t>(t.size(2), 1); };
+  const c10::DeviceGuard g(a.device());
+  check_status(ak_gemm_batched(dtype_code(a, op), a.data_ptr(), b.data_ptr(), c.data_ptr(), Z, M, N, K, ld(a),
+                               ld(b), ld(c), a.stride(0), b.stride(0), c.stride(0), b_trans ? 1 : 0, stream_of(a)),
+               "ak_gemm_batched");
+}
+
 int64_t ak_op_gemm_workspace_bytes(int64_t dtype, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                                    int64_t ldc, bool b_trans) {
   return ak_gemm_workspace_bytes((int)dtype, M, N, K, lda, ldb, ldc, b_trans ? 1 : 0);
@@ -290,6 +315,8 @@ TORCH_LIBRARY_EXPAND(TORCH_EXTENSION_NAME, ops) {
   ops.impl("reduce_max", c10::kCUDA, &ak_op_reduce_max);
   ops.def("gemm(Tensor! c, Tensor a, Tensor b, bool b_trans, Tensor(w!)? workspace) -> ()");
   ops.impl("gemm", c10::kCUDA, &ak_op_gemm);
+  ops.def("gemm_batched(Tensor! c, Tensor a, Tensor b, bool b_trans) -> ()");
+  ops.impl("gemm_batched", c10::kCUDA, &ak_op_gemm_batched);
   ops.def("gemm_workspace_bytes(int dtype, int M, int N, int K, int lda, int ldb, int ldc, bool b_trans) -> int");
   ops.impl("gemm_workspace_bytes", &ak_op_gemm_workspace_bytes);
   ops.def("mlp_gate_up(Tensor! h, Tensor x, Tensor w_gate, Tensor w_up, int activation) -> ()");

@@ -23,6 +23,7 @@ void ak_op_reduce_sum(at::Tensor& y, const at::Tensor& x, int64_t outer, int64_t
 void ak_op_reduce_max(at::Tensor& y, const at::Tensor& x, int64_t outer, int64_t reduce, int64_t inner);
 void ak_op_gemm(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, bool b_trans,
                 const std::optional<at::Tensor>& workspace);
+void ak_op_gemm_batched(at::Tensor& c, const at::Tensor& a, const at::Tensor& b, bool b_trans);
 int64_t ak_op_gemm_workspace_bytes(int64_t dtype, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                                    int64_t ldc, bool b_trans);
 void ak_op_mlp_gate_up(at::Tensor& h, const at::Tensor& x, const at::Tensor& w_gate,

@@ -97,6 +97,19 @@ def gemm(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor, b_trans: bool,
          int(bool(b_trans)), M=M, N=N, K=K, b_trans=b_trans, dtype=a.dtype)
 
 
+def gemm_batched(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor, b_trans: bool) -> None:
+    """c [Z, M, N] = a [Z, M, K] @ op(b) for each batch item z: b stored [Z, K, N] (b_trans False) or
+    [Z, N, K] (True); unit stride along each last dim, any row and batch strides (0 broadcasts)."""
+    Z, M, K = a.shape
+    N = b.shape[1] if b_trans else b.shape[2]
+
+    def ld(t):
+        return t.stride(1) if t.shape[1] > 1 else max(t.shape[2], 1)
+    _run("ak_gemm_batched", a, _code(a, "matmul"), a.data_ptr(), b.data_ptr(), c.data_ptr(), Z, M, N, K, ld(a),
+         ld(b), ld(c), a.stride(0), b.stride(0), c.stride(0), int(bool(b_trans)), Z=Z, M=M, N=N, K=K,
+         b_trans=b_trans, dtype=a.dtype)
+
+
 def gemm_bias(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor, b_trans: bool) -> None:
     """c = a @ op(b) + bias [N], the bias added to the fp32 accumulator (one rounding)."""
     M, K = a.shape

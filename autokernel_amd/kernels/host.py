@@ -224,13 +224,32 @@ def matmul(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
         lead = A.shape[:-1]
         A2 = A.reshape(-1, A.shape[-1]) if A.dim() > 2 else A
         return _gemm(A2, B, split_k=True).view(*lead, B.shape[-1])
+    # batched: broadcast batch dims (a stride of 0 shares an operand), one batched launch
     batch = torch.broadcast_shapes(A.shape[:-2], B.shape[:-2])
-    Ab = A.expand(*batch, *A.shape[-2:]).reshape(-1, *A.shape[-2:])
-    Bb = B.expand(*batch, *B.shape[-2:]).reshape(-1, *B.shape[-2:])
-    C = torch.empty((Ab.shape[0], A.shape[-2], B.shape[-1]), device=A.device, dtype=A.dtype)
-    for i in range(Ab.shape[0]):
-        _gemm(Ab[i], Bb[i], out=C[i], split_k=True)
-    return C.view(*batch, A.shape[-2], B.shape[-1])
+    M, K = A.shape[-2:]
+    K2, N = B.shape[-2:]
+    if K != K2:
+        raise ValueError(f"matmul: shapes {tuple(A.shape)} and {tuple(B.shape)} do not align")
+    if A.dtype != B.dtype:
+        raise ValueError(f"matmul: dtype mismatch {A.dtype} vs {B.dtype}")
+    nb = math.prod(batch)
+    C = torch.empty((nb, M, N), device=A.device, dtype=A.dtype)
+    if nb == 0 or M == 0 or N == 0:
+        return C.view(*batch, M, N)
+    if K == 0:
+        return C.zero_().view(*batch, M, N)
+    Ab = A.expand(*batch, M, K).reshape(nb, M, K)
+    Bb = B.expand(*batch, K, N).reshape(nb, K, N)
+    if not (Ab.stride(2) == 1 and Ab.stride(1) >= max(K, 1)):
+        Ab = Ab.contiguous()
+    if Bb.stride(2) == 1 and Bb.stride(1) >= max(N, 1):
+        Bs, bt = Bb, False
+    elif Bb.stride(1) == 1 and Bb.stride(2) >= max(K, 1):
+        Bs, bt = Bb.transpose(1, 2), True  # the stored [N, K] matrices
+    else:
+        Bs, bt = Bb.contiguous(), False
+    ops.gemm_batched(C, Ab, Bs, bt)
+    return C.view(*batch, M, N)
 
 
 def fused_mlp(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,

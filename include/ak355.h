@@ -169,6 +169,18 @@ int ak_gemm(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t
             int64_t lda, int64_t ldb, int64_t ldc, int b_trans, hipStream_t stream);
 
 /*
+ * Batched GEMM: for z in [0, batch), C_z = A_z * op(B_z) as ak_gemm computes each product, where
+ * X_z starts stride_x elements after X_{z-1}. A stride of 0 shares A or B across the batch (a
+ * broadcast operand). C's items must not overlap. One launch for the whole batch (the batch is the
+ * grid's third dimension) on the f16 / bf16 kernels; fp32 runs ak_gemm per item.
+ * Replaces: reference.py:10-12 matmul_ref for operands with batch dimensions (torch.matmul's
+ *           broadcast batched product), one launch instead of one per batch item.
+ */
+int ak_gemm_batched(int dtype, const void* A, const void* B, void* C, int64_t batch, int64_t M,
+                    int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t stride_a,
+                    int64_t stride_b, int64_t stride_c, int b_trans, hipStream_t stream);
+
+/*
  * Split-K GEMM for grids that leave most compute units idle (few output tiles, long K), e.g.
  * 1024 x 1024 x 8192. Same arguments and result semantics as ak_gemm (fp32 accumulation, one output
  * rounding; deterministic), plus a caller-owned fp32 workspace.

@@ -31,6 +31,7 @@ SCHEMAS = {
     "reduce_sum": "(Tensor($0! -> ) y, Tensor x, int outer, int reduce, int inner) -> ()",
     "reduce_max": "(Tensor($0! -> ) y, Tensor x, int outer, int reduce, int inner) -> ()",
     "gemm": "(Tensor($0! -> ) c, Tensor a, Tensor b, bool b_trans, Tensor(w!)? workspace) -> ()",
+    "gemm_batched": "(Tensor($0! -> ) c, Tensor a, Tensor b, bool b_trans) -> ()",
     "gemm_workspace_bytes": "(int dtype, int M, int N, int K, int lda, int ldb, int ldc, bool b_trans) -> int",
     "mlp_gate_up": "(Tensor($0! -> ) h, Tensor x, Tensor w_gate, Tensor w_up, int activation) -> ()",
     "flash_attn_fwd": "(Tensor($0! -> ) o, Tensor q, Tensor k, Tensor v, bool causal, float sm_scale) -> ()",

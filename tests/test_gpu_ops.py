@@ -273,6 +273,44 @@ def test_matmul_linear_layout_and_strides(gpu):
     assert_close(kernels.get("matmul")(A.to(gpu), B.to(gpu)), R.matmul_ref(A.float(), B.float()).half(), 1e-2, 1e-2, "batched")
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+def test_matmul_batched_one_launch(gpu, dt):
+    """torch.matmul's batched and broadcast forms run as one ak_gemm_batched launch (the batch on the
+    grid's third dimension): against the oracle at the table's tolerance, and bit-identical to the
+    same products run one 2-D GEMM at a time (the same per-element arithmetic). Cases: [K, N] and
+    transposed ([N, K] stored) B, a 2-D operand broadcast over the batch (batch stride 0), two
+    broadcast batch dims, attention-shaped products, K not a multiple of 8 (the register-staged
+    kernel), an empty batch and K = 0."""
+    from autokernel_amd.kernels.host import _gemm
+    g = torch.Generator().manual_seed(21)
+    tol = 1e-4 if dt == torch.float32 else 2e-2
+
+    def r(*s):
+        return (torch.randn(*s, generator=g) / max(s[-1], 1) ** 0.5).to(dt)
+    cases = [(r(3, 64, 128), r(3, 128, 96)),
+             (r(4, 70, 256), r(4, 96, 256).transpose(-1, -2)),     # B read as stored [N, K] matrices
+             (r(70, 256), r(5, 256, 136)),                         # A broadcast (batch stride 0)
+             (r(5, 96, 256), r(256, 136)),                         # B 2-D: flattened into one GEMM
+             (r(6, 64, 512), r(512, 96).expand(6, 512, 96)),       # B broadcast (batch stride 0)
+             (r(2, 1, 40, 64), r(1, 3, 64, 72)),                   # two broadcast batch dims
+             (r(32, 512, 64), r(32, 64, 512)),                     # attention scores shape
+             (r(32, 512, 512), r(32, 512, 64)),
+             (r(3, 33, 100), r(3, 100, 40)),                       # K % 8 != 0
+             (r(0, 8, 64), r(0, 64, 8)), (r(2, 8, 0), r(2, 0, 8))]
+    for A, B in cases:
+        out = kernels.get("matmul")(A.to(gpu), B.to(gpu)).cpu()
+        exp = R.matmul_ref(A.float(), B.float()).to(dt)
+        what = f"{tuple(A.shape)} @ {tuple(B.shape)} {dt}"
+        assert out.shape == exp.shape, what
+        assert_close(out, exp, tol, tol, what)
+        if B.dim() >= 3 and out.numel() and A.shape[-1]:
+            batch = torch.broadcast_shapes(A.shape[:-2], B.shape[:-2])
+            Ab = A.expand(*batch, *A.shape[-2:]).reshape(-1, *A.shape[-2:]).to(gpu)
+            Bb = B.expand(*batch, *B.shape[-2:]).reshape(-1, *B.shape[-2:]).to(gpu)
+            one = torch.stack([_gemm(Ab[i], Bb[i]) for i in range(Ab.shape[0])]).cpu()
+            assert torch.equal(out.reshape(one.shape), one), what
+
+
 @pytest.mark.parametrize("M,N,K", [(2048, 6144, 256), (500, 1100, 320), (256, 192, 64)])
 def test_matmul_linear_wide_tiles(gpu, M, N, K):
     """nn.Linear-layout shapes whose best tiling is 256x192 (a fused QKV projection's 2048 x 6144,
