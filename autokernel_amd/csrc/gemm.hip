@@ -189,9 +189,54 @@ __device__ __forceinline__ float gate_up(float g_acc, float u_acc) {
 //     of 4, so the four columns never straddle a head or the rot_cols boundary.
 // The side values (R, or the cos / sin pairs) of every fragment are loaded first, then combined
 // and stored, so their latency is paid once per tile rather than once per fragment.
-// VEC: four in-range columns of C (or R) move as one 8-byte access wherever that access is 8-byte
-// aligned, checked per access: any leading dimension works, and rows whose start is not 8-byte
-// aligned (an odd ldc, e.g. a 50257-column vocabulary projection) take element accesses.
+// Stores: the results of fragments 2p and 2p + 1 (columns 32p + 4g + 0..3 and 32p + 16 + 4g + 0..3
+// in lane group g = lane / 16) are packed to the element type and regrouped across the four lane
+// groups (regroup8), so each lane stores 8 consecutive columns 32p + 8g + 0..7 of its row: one
+// 16-byte store where C is 16-byte aligned, which fills the 64-byte requests (4 lanes x 16 bytes
+// per row) that 8-byte stores half-fill.
+// VEC: in-range columns of C (or R) move as 8- / 16-byte accesses wherever the access is that
+// aligned, checked per access: any leading dimension works, and rows whose start is not aligned
+// (an odd ldc, e.g. a 50257-column vocabulary projection) take narrower accesses.
+// Regroup two fragments' packed columns across the 16-lane groups of a wave. On entry lane group g
+// (lanes 16g .. 16g + 15) holds 4-column group g of fragment x and of fragment y, i.e. groups g and
+// 4 + g of their 32 columns; on exit it holds group 2g in x and group 2g + 1 in y. Lanes keep their
+// row (lane % 16). permlane32_swap exchanges x's upper half-wave with y's lower one
+// (x = [x0 x1 y0 y1], y = [x2 x3 y2 y3] by lane group), permlane16_swap x's odd lane groups with
+// y's even ones (x = [x0 x2 y0 y2], y = [x1 x3 y1 y3]).
+__device__ __forceinline__ void regroup8(uint32_t& x, uint32_t& y) {
+  const auto h = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+  const auto q = __builtin_amdgcn_permlane16_swap(h[0], h[1], false, false);
+  x = q[0];
+  y = q[1];
+}
+
+// Store the first W (4 or 8) 16-bit elements of o (element e in dword e / 2, low half first) to
+// cp[0 .. W - 1], the first `valid` of them only: one 16- or 8-byte store where the address allows
+// (VEC), else dword or element stores.
+template <bool VEC, int W>
+__device__ __forceinline__ void store_cols(uint16_t* cp, int valid, const u32x4& o) {
+  const uintptr_t a = (uintptr_t)cp;
+  if (VEC && valid >= W) {
+    if (W == 8 && (a & 15u) == 0) {
+      *reinterpret_cast<u32x4*>(cp) = o;
+      return;
+    }
+    if ((a & 7u) == 0) {
+      *reinterpret_cast<u32x2*>(cp) = u32x2{o[0], o[1]};
+      if (W == 8) *reinterpret_cast<u32x2*>(cp + 4) = u32x2{o[2], o[3]};
+      return;
+    }
+    if ((a & 3u) == 0) {
+#pragma unroll
+      for (int d = 0; d < W / 2; ++d) reinterpret_cast<uint32_t*>(cp)[d] = o[d];
+      return;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < W; ++e)
+    if (e < valid) cp[e] = (uint16_t)(o[e >> 1] >> ((e & 1) * 16));
+}
+
 template <typename T, int NB, int EPI, bool VEC, int FM, int FN, int MST = 16, int NST = 16>
 __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const uint16_t* __restrict__ R,
                                               int64_t ldc, int M, int N, int mb, int nb,
@@ -267,10 +312,11 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
       }
     }
   }
+  static_assert(NST == 16, "fragment pairs regroup 16-column fragments");
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int m = mb + i * MST;
-    if (m >= M) continue;
+    uint32_t lo[FN], hi[FN];  // packed columns 0, 1 and 2, 3 of each fragment
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int n = nb + j * NST;
@@ -299,16 +345,28 @@ __device__ __forceinline__ void tile_epilogue(uint16_t* __restrict__ C, const ui
           rope_rotate(v[2], v[3], side_c[i][j][1], side_s[i][j][1]);
         }
       }
-      uint16_t* cp = C + (int64_t)m * ldc + n;
-      if (VEC && n + 3 < N && ((uintptr_t)cp & 7u) == 0) {
-        u32x2 o;
-        o[0] = (uint32_t)T::from_f(v[0]) | ((uint32_t)T::from_f(v[1]) << 16);
-        o[1] = (uint32_t)T::from_f(v[2]) | ((uint32_t)T::from_f(v[3]) << 16);
-        *reinterpret_cast<u32x2*>(cp) = o;
-      } else {
+      lo[j] = (uint32_t)T::from_f(v[0]) | ((uint32_t)T::from_f(v[1]) << 16);
+      hi[j] = (uint32_t)T::from_f(v[2]) | ((uint32_t)T::from_f(v[3]) << 16);
+    }
+    // fragment pairs: 8 consecutive columns per lane (the shuffles run on every lane, before the
+    // row test)
+    const int g = (lane_id() >> 4) & 3;
+    const int nq = nb - 4 * g + 8 * g;  // lane group g's first column of pair 0
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (n + e < N) cp[e] = T::from_f(v[e]);
+    for (int j = 0; j + 1 < FN; j += 2) {
+      regroup8(lo[j], lo[j + 1]);
+      regroup8(hi[j], hi[j + 1]);
+      if (m < M) {
+        const u32x4 o = {lo[j], hi[j], lo[j + 1], hi[j + 1]};
+        const int n = nq + j * NST;
+        store_cols<VEC, 8>(C + (int64_t)m * ldc + n, N - n, o);
+      }
+    }
+    if constexpr (FN % 2 == 1) {
+      if (m < M) {
+        const int n = nb + (FN - 1) * NST;
+        const u32x4 o = {lo[FN - 1], hi[FN - 1], 0u, 0u};
+        store_cols<VEC, 4>(C + (int64_t)m * ldc + n, N - n, o);
       }
     }
   }
