@@ -175,6 +175,13 @@ def test_exported_layouts_match_kernels(gpu):
     assert torch.equal(host.matmul(x, W.t()), kernels.get("matmul")(x, W.t()))
     big = torch.randn(300, 300, generator=g).half().to(gpu)
     assert torch.equal(host.matmul(big[:, :256], W.t()), kernels.get("matmul")(big[:, :256], W.t()))
+    a = torch.randn(3, 4, 70, 96, generator=g).half().to(gpu)  # batched: the gemm_batched op
+    b = torch.randn(4, 96, 136, generator=g).half().to(gpu)    # broadcast over a's first dim
+    assert torch.equal(host.matmul(a, b), kernels.get("matmul")(a, b))
+    bt = torch.randn(4, 136, 96, generator=g).half().to(gpu).transpose(-1, -2)  # stored [N, K] items
+    assert torch.equal(host.matmul(a, bt), kernels.get("matmul")(a, bt))
+    assert torch.equal(host.matmul(a, bt), torch.stack([torch.stack([kernels.get("matmul")(a[i, j], bt[j])
+                                                                     for j in range(4)]) for i in range(3)]))
     q = torch.randn(2, 200, 8, 128, generator=g).half().to(gpu).transpose(1, 2)
     k = torch.randn(2, 200, 2, 128, generator=g).half().to(gpu).transpose(1, 2)
     v = torch.randn(2, 200, 2, 128, generator=g).half().to(gpu).transpose(1, 2)
