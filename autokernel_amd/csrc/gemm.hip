@@ -1029,9 +1029,12 @@ struct DmaPlan {
   // Three 64-deep stages where they fit beside 8 waves, else two. Measured (bf16, NT):
   // 2048x4096x4096 on 256x128 tiles 83.5 us two-stage -> 63.4 us three-stage; 4096^3 on 256x256
   // 107.4 us two-stage (four 32-deep stages: 121.2 us, the doubled barrier count outweighs the
-  // deeper queue).
+  // deeper queue). The 64x64 tile (4 waves, 16 KB stages, picked for grids that larger tiles leave
+  // mostly idle) waits on transfer latency, not MFMAs: four stages keep three tiles in flight
+  // (cold, f16: 1024^3 15.5 -> 10.8 us, 2048x768x3072 37.0 -> 29.8 us, 2048x1024x1024 16.6 ->
+  // 14.6 us; four stages on 128x128 tiles gained nothing).
   static constexpr int BKD = 64;
-  static constexpr int NS = (kFit64 >= 3 && NW == 8) ? 3 : 2;
+  static constexpr int NS = BM == 64 ? 4 : (kFit64 >= 3 && NW == 8) ? 3 : 2;
 };
 
 template <typename T, int BM, int BN, int WM, int WN, int NB, int EPI, bool BKN>
