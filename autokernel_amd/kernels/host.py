@@ -180,6 +180,32 @@ def reduce_max(x: torch.Tensor, dim: int = -1) -> torch.Tensor:
     return _reduce(x, dim, True)
 
 
+# f16 / bf16 operands that the LDS-DMA GEMM cannot read as 16-byte chunks (K or a row stride not a
+# multiple of 8 elements, a base that is not 16-byte aligned, a [K, N] B with N % 8 != 0) would take
+# the register-staged kernel's element loads, 4-5x slower from 255^3 up (f16 1023^3: 151 us against
+# 28 us repacked; 4095^3: 882 against 228 us). Above this size they are copied once into zero-padded
+# operands whose K is a multiple of 64. The extra products are exact zeros at the end of each sum,
+# so the result is the same.
+_REPACK_MIN_MNK = 1 << 21
+
+
+def _ld(t: torch.Tensor) -> int:
+    return t.stride(0) if t.shape[0] > 1 else max(t.shape[1], 1)
+
+
+def _repack(A: torch.Tensor, Bs: torch.Tensor, bt: bool, N: int, K: int):
+    """A [M, Kp] and B as [N, Kp] (bt) or [Kp, N] (a [K, N] B with N % 8 == 0), zero-padded."""
+    Kp = -(-K // 64) * 64
+    A = torch.nn.functional.pad(A, (0, Kp - K)).contiguous()
+    if bt:
+        Bs = torch.nn.functional.pad(Bs, (0, Kp - K)).contiguous()
+    elif N % 8 == 0:
+        Bs = torch.nn.functional.pad(Bs, (0, 0, 0, Kp - K)).contiguous()
+    else:
+        Bs, bt = torch.nn.functional.pad(Bs.t(), (0, Kp - K)).contiguous(), True
+    return A, Bs, bt, Kp
+
+
 def _gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, split_k: bool = False) -> torch.Tensor:
     """C = A @ B for 2-D A [M, K] and B [K, N]; a transposed [N, K] view of B is read in place.
     split_k: grids that leave most CUs idle split K (the matmul op does; fused_mlp does not)."""
@@ -200,12 +226,14 @@ def _gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, spl
     C = out if out is not None else torch.empty((M, N), device=A.device, dtype=A.dtype)
     if K == 0:
         return C.zero_()
+    if A.dtype != torch.float32 and M * N * K >= _REPACK_MIN_MNK and not (
+            K % 8 == 0 and _ld(A) % 8 == 0 and _ld(Bs) % 8 == 0 and A.data_ptr() % 16 == 0
+            and Bs.data_ptr() % 16 == 0 and (bt or N % 8 == 0)):
+        A, Bs, bt, K = _repack(A, Bs, bt, N, K)
     ws = None
     if split_k:
-        def ld(t):
-            return t.stride(0) if t.shape[0] > 1 else max(t.shape[1], 1)
         code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[A.dtype]
-        nbytes = ops.gemm_workspace_bytes(code, M, N, K, ld(A), ld(Bs), ld(C), bt)
+        nbytes = ops.gemm_workspace_bytes(code, M, N, K, _ld(A), _ld(Bs), _ld(C), bt)
         if nbytes > 0:
             ws = torch.empty(nbytes // 4, device=A.device, dtype=torch.float32)
     ops.gemm(C, A, Bs, bt, ws)

@@ -273,6 +273,38 @@ def test_matmul_linear_layout_and_strides(gpu):
     assert_close(kernels.get("matmul")(A.to(gpu), B.to(gpu)), R.matmul_ref(A.float(), B.float()).half(), 1e-2, 1e-2, "batched")
 
 
+@pytest.mark.parametrize("M,N,K,layout,dt", [
+    (1023, 1023, 1023, "kn", torch.float16),      # K, lda and ldb odd
+    (600, 300, 515, "nk", torch.bfloat16),        # nn.Linear-layout B, K odd
+    (700, 1001, 512, "kn", torch.float16),        # [K, N] B with N % 8 != 0
+    (257, 1030, 1024, "kn", torch.bfloat16),      # N % 8 == 6
+    (512, 640, 512, "offset", torch.float16),     # A's base 2 bytes past a 16-byte boundary
+    (100, 90, 70, "kn", torch.float16),           # below the repack size: the element-load kernel
+])
+def test_matmul_misaligned_operands_repacked(gpu, M, N, K, layout, dt):
+    """Operands the 16-byte loads cannot read are repacked by kernel_fn (zero-padded K, [N, K] or
+    [K, N] copies): the result equals the register-staged kernel run on the original operands bit
+    for bit (the padding adds exact zeros at the end of each sum), and the oracle at the tolerance."""
+    from autokernel_amd.kernels import _ops
+    g = torch.Generator().manual_seed(M + N + K)
+    A = (torch.randn(M, K + (1 if layout == "offset" else 0), generator=g) / K ** 0.5).to(dt)
+    if layout == "nk":
+        W = torch.randn(N, K, generator=g).to(dt)
+        Bd, Bs, bt = W.to(gpu).t(), W.to(gpu), True
+        Bf = W.float().T
+    else:
+        Bk = torch.randn(K, N, generator=g).to(dt)
+        Bd, Bs, bt = Bk.to(gpu), Bk.to(gpu), False
+        Bf = Bk.float()
+    Ad = A.to(gpu)[:, 1:] if layout == "offset" else A.to(gpu)
+    Af = A[:, 1:].float() if layout == "offset" else A.float()
+    out = kernels.get("matmul")(Ad, Bd)
+    assert_close(out, R.matmul_ref(Af, Bf).to(dt), 2e-2, 2e-2, f"misaligned {M}x{N}x{K} {layout} {dt}")
+    direct = torch.empty(M, N, device=gpu, dtype=dt)
+    _ops.gemm(direct, Ad, Bs, bt, None)
+    assert torch.equal(out, direct), f"repacked != element-load kernel {M}x{N}x{K} {layout} {dt}"
+
+
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
 def test_matmul_batched_one_launch(gpu, dt):
     """torch.matmul's batched and broadcast forms run as one ak_gemm_batched launch (the batch on the
