@@ -825,12 +825,19 @@ template <bool BT>
 __global__ __launch_bounds__(256) void gemm_f32(const float* __restrict__ A, const float* __restrict__ B,
                                                 float* __restrict__ C, int M, int N, int K,
                                                 int64_t lda, int64_t ldb, int64_t ldc, int tiles_m,
-                                                int tiles_n) {
+                                                int tiles_n, int64_t batch_a, int64_t batch_b,
+                                                int64_t batch_c) {
   constexpr int BM = kF32BM, BN = kF32BN, BK = kF32BK;
   constexpr int PA = BK + 1;
   constexpr int PBN = BN + 16;
   __shared__ float sA[2][BM * PA];
   __shared__ float sB[2][BT ? BN * PA : BK * PBN];
+  if (gridDim.z > 1) {  // batch item blockIdx.z (ak_gemm_batched)
+    const int64_t z = blockIdx.z;
+    A += z * batch_a;
+    B += z * batch_b;
+    C += z * batch_c;
+  }
   int tm, tn;
   tile_coords(tiles_m, tiles_n, &tm, &tn);
   const int m0 = tm * BM, n0 = tn * BN;
@@ -1190,15 +1197,18 @@ static int launch_gemm16_splitk(const void* A, const void* B, void* C, int64_t M
   return record_launch();
 }
 
+// batch > 1: grid z is the batch item, whose operands start z * batch_x elements further
 static int launch_gemm32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
-                         int64_t lda, int64_t ldb, int64_t ldc, bool bt, hipStream_t s) {
+                         int64_t lda, int64_t ldb, int64_t ldc, bool bt, hipStream_t s, int batch = 1,
+                         int64_t batch_a = 0, int64_t batch_b = 0, int64_t batch_c = 0) {
   const int tiles_m = (int)cdiv(M, kF32BM), tiles_n = (int)cdiv(N, kF32BN);
+  const dim3 grid(tiles_m * tiles_n, 1, batch);
   if (bt)
-    gemm_f32<true><<<tiles_m * tiles_n, 256, 0, s>>>((const float*)A, (const float*)B, (float*)C, (int)M,
-                                                     (int)N, (int)K, lda, ldb, ldc, tiles_m, tiles_n);
+    gemm_f32<true><<<grid, 256, 0, s>>>((const float*)A, (const float*)B, (float*)C, (int)M, (int)N, (int)K, lda,
+                                        ldb, ldc, tiles_m, tiles_n, batch_a, batch_b, batch_c);
   else
-    gemm_f32<false><<<tiles_m * tiles_n, 256, 0, s>>>((const float*)A, (const float*)B, (float*)C, (int)M,
-                                                      (int)N, (int)K, lda, ldb, ldc, tiles_m, tiles_n);
+    gemm_f32<false><<<grid, 256, 0, s>>>((const float*)A, (const float*)B, (float*)C, (int)M, (int)N, (int)K, lda,
+                                         ldb, ldc, tiles_m, tiles_n, batch_a, batch_b, batch_c);
   return record_launch();
 }
 
@@ -1332,9 +1342,7 @@ extern "C" int ak_gemm_batched(int dtype, const void* A, const void* B, void* C,
     char* c = (char*)C + z0 * stride_c * esz;
     int st = AK_OK;
     if (dtype == AK_F32) {
-      for (int64_t z = 0; z < nz && st == AK_OK; ++z)
-        st = launch_gemm32(a + z * stride_a * 4, b + z * stride_b * 4, c + z * stride_c * 4, M, N, K, lda, ldb,
-                           ldc, bt, stream);
+      st = launch_gemm32(a, b, c, M, N, K, lda, ldb, ldc, bt, stream, (int)nz, stride_a, stride_b, stride_c);
     } else {
       EpiArgs ep;
       ep.batch = (int)nz;

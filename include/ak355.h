@@ -172,7 +172,7 @@ int ak_gemm(int dtype, const void* A, const void* B, void* C, int64_t M, int64_t
  * Batched GEMM: for z in [0, batch), C_z = A_z * op(B_z) as ak_gemm computes each product, where
  * X_z starts stride_x elements after X_{z-1}. A stride of 0 shares A or B across the batch (a
  * broadcast operand). C's items must not overlap. One launch for the whole batch (the batch is the
- * grid's third dimension) on the f16 / bf16 kernels; fp32 runs ak_gemm per item.
+ * grid's third dimension), for fp32 as for f16 / bf16.
  * Replaces: reference.py:10-12 matmul_ref for operands with batch dimensions (torch.matmul's
  *           broadcast batched product), one launch instead of one per batch item.
  */
