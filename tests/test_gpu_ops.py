@@ -824,9 +824,29 @@ def _gelu_matches_torch(out: torch.Tensor, exp: torch.Tensor, what: str) -> None
     position in its vectorised loop."""
     ulps = _ulps16(out, exp)
     n_diff = int((ulps != 0).sum())
-    print(f"{what}: {n_diff} of {out.numel()} elements differ from F.gelu (max {int(ulps.max())} ulp)", flush=True)
+    print(f"{what}: {n_diff} of {out.numel()} elements differ from torch (max {int(ulps.max())} ulp)", flush=True)
     assert int(ulps.max()) <= 1, what
     assert n_diff <= max(4, out.numel() // 100000), what
+
+
+def test_gate_up_activation_every_value(gpu):
+    """Every finite f16 / bf16 value through ak_mlp_gate_up's SiLU and GELU (the epilogue's lookup
+    tables): with x the [256, 256] identity, gate[m, n] = W_gate[n, m] exactly and up = 1 (W_up all
+    ones), so h holds act(value) rounded once. Against torch's own F.silu / F.gelu of the same
+    values on the GPU under _gelu_matches_torch's rule."""
+    from autokernel_amd.kernels.fused_mlp import gate_up
+    F = torch.nn.functional
+    for dt in (torch.float16, torch.bfloat16):
+        vals = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(dt)
+        vals = vals[torch.isfinite(vals)]
+        N = vals.numel() // 256
+        W = vals.view(N, 256).to(gpu)
+        x = torch.eye(256, dtype=dt, device=gpu)
+        ones = torch.ones(N, 256, dtype=dt, device=gpu)
+        Wt = W.t().contiguous()
+        for act, ref in (("silu", F.silu), ("gelu", F.gelu)):
+            h = gate_up(x, W, ones, act)
+            _gelu_matches_torch(h, ref(Wt), f"every {dt} value through the gate/up {act}")
 
 
 @pytest.mark.parametrize("M,N,K", [(2048, 3072, 768), (8 * 512, 768, 3072), (300, 520, 200), (257, 77, 96),
