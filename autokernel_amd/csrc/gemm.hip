@@ -211,26 +211,20 @@ __device__ __forceinline__ void regroup8(uint32_t& x, uint32_t& y) {
 }
 
 // Store the first W (4 or 8) 16-bit elements of o (element e in dword e / 2, low half first) to
-// cp[0 .. W - 1], the first `valid` of them only: one 16- or 8-byte store where the address allows
-// (VEC), else dword or element stores.
+// cp[0 .. W - 1], the first `valid` of them only. With all W in range (VEC) it is one 16- or 8-byte
+// store at whatever 2-byte alignment cp has: global memory on this target takes multi-dword
+// accesses at any alignment (the HSA code object is built with unaligned-access-mode, which is why
+// the compiler emits one global_store_dwordx4 for a 2-byte-aligned pointer here). Rows whose start
+// is not 16-byte aligned (an odd ldc, e.g. a 50257-column vocabulary projection) took 47 % longer
+// with stores narrowed to their alignment.
+typedef u32x4 u32x4_a2 __attribute__((aligned(2)));
+typedef u32x2 u32x2_a2 __attribute__((aligned(2)));
 template <bool VEC, int W>
 __device__ __forceinline__ void store_cols(uint16_t* cp, int valid, const u32x4& o) {
-  const uintptr_t a = (uintptr_t)cp;
   if (VEC && valid >= W) {
-    if (W == 8 && (a & 15u) == 0) {
-      *reinterpret_cast<u32x4*>(cp) = o;
-      return;
-    }
-    if ((a & 7u) == 0) {
-      *reinterpret_cast<u32x2*>(cp) = u32x2{o[0], o[1]};
-      if (W == 8) *reinterpret_cast<u32x2*>(cp + 4) = u32x2{o[2], o[3]};
-      return;
-    }
-    if ((a & 3u) == 0) {
-#pragma unroll
-      for (int d = 0; d < W / 2; ++d) reinterpret_cast<uint32_t*>(cp)[d] = o[d];
-      return;
-    }
+    if constexpr (W == 8) *reinterpret_cast<u32x4_a2*>(cp) = o;
+    else *reinterpret_cast<u32x2_a2*>(cp) = u32x2{o[0], o[1]};
+    return;
   }
 #pragma unroll
   for (int e = 0; e < W; ++e)
