@@ -194,9 +194,9 @@ __device__ __forceinline__ float gate_up(float g_acc, float u_acc) {
 // groups (regroup8), so each lane stores 8 consecutive columns 32p + 8g + 0..7 of its row: one
 // 16-byte store where C is 16-byte aligned, which fills the 64-byte requests (4 lanes x 16 bytes
 // per row) that 8-byte stores half-fill.
-// VEC: in-range columns of C (or R) move as 8- / 16-byte accesses wherever the access is that
-// aligned, checked per access: any leading dimension works, and rows whose start is not aligned
-// (an odd ldc, e.g. a 50257-column vocabulary projection) take narrower accesses.
+// VEC: a lane's 8 in-range columns of C are one 16-byte store at any alignment (store_cols), so
+// any leading dimension works (an odd ldc, e.g. a 50257-column vocabulary projection); R's four
+// columns load as one 8-byte access where that is 8-byte aligned, as elements otherwise.
 // Regroup two fragments' packed columns across the 16-lane groups of a wave. On entry lane group g
 // (lanes 16g .. 16g + 15) holds 4-column group g of fragment x and of fragment y, i.e. groups g and
 // 4 + g of their 32 columns; on exit it holds group 2g in x and group 2g + 1 in y. Lanes keep their
