@@ -95,6 +95,13 @@ def test_invalid_arguments_rejected_on_host(lib):
     assert lib.ak_cross_entropy_noalloc(1, x, x, None, 4, 8, -100, None) == _lib.AK_EINVAL   # no output
     assert lib.ak_cross_entropy_noalloc(7, x, x, x, 4, 8, -100, None) == _lib.AK_EINVAL      # bad dtype
     assert lib.ak_gemm_ws(1, x, x, x, 0, 4, 4, 4, 4, 4, 1, None, 0, None) == _lib.AK_OK  # empty -> ak_gemm
+    bat = lib.ak_gemm_batched  # (dtype, A, B, C, batch, M, N, K, lda, ldb, ldc, sa, sb, sc, b_trans, stream)
+    assert bat(1, x, x, y, -1, 4, 4, 4, 4, 4, 4, 16, 16, 16, 0, None) == _lib.AK_EINVAL   # negative batch
+    assert bat(1, x, x, y, 0, 4, 4, 4, 4, 4, 4, 16, 16, 16, 0, None) == _lib.AK_OK        # empty batch
+    assert bat(1, x, x, y, 2, 4, 4, 4, 4, 4, 4, 16, 16, 8, 0, None) == _lib.AK_EINVAL     # C items overlap
+    assert bat(1, x, x, y, 2, 4, 4, 4, 4, 4, 4, -16, 16, 16, 0, None) == _lib.AK_EINVAL   # negative stride
+    assert bat(1, x, x, y, 2, 4, 4, 4, 2, 4, 4, 16, 16, 16, 0, None) == _lib.AK_EINVAL    # lda < K
+    assert bat(7, x, x, y, 2, 4, 4, 4, 4, 4, 4, 16, 16, 16, 0, None) == _lib.AK_EINVAL    # bad dtype code
     rope = lib.ak_gemm_rope
     assert rope(1, x, x, y, 4, 8, 4, 4, 4, 8, 1, x, x, 4, 6, 6, None) == _lib.AK_EINVAL  # head_dim % 4
     assert rope(1, x, x, y, 4, 8, 4, 4, 4, 8, 1, x, x, 4, 4, 6, None) == _lib.AK_EINVAL  # rot_cols % head_dim
