@@ -311,8 +311,9 @@ def test_matmul_batched_one_launch(gpu, dt):
     grid's third dimension): against the oracle at the table's tolerance, and bit-identical to the
     same products run one 2-D GEMM at a time (the same per-element arithmetic). Cases: [K, N] and
     transposed ([N, K] stored) B, a 2-D operand broadcast over the batch (batch stride 0), two
-    broadcast batch dims, attention-shaped products, K not a multiple of 8 (the register-staged
-    kernel), an empty batch and K = 0."""
+    broadcast batch dims, attention-shaped products, K not a multiple of 8 and a [K, N] B with
+    N % 8 != 0 (the register-staged kernel; per item, the 2-D path's repacked LDS-DMA products give
+    the same bits), an empty batch and K = 0."""
     from autokernel_amd.kernels.host import _gemm
     g = torch.Generator().manual_seed(21)
     tol = 1e-4 if dt == torch.float32 else 2e-2
@@ -328,6 +329,8 @@ def test_matmul_batched_one_launch(gpu, dt):
              (r(32, 512, 64), r(32, 64, 512)),                     # attention scores shape
              (r(32, 512, 512), r(32, 512, 64)),
              (r(3, 33, 100), r(3, 100, 40)),                       # K % 8 != 0
+             (r(8, 128, 130), r(8, 130, 256)),                     # K % 8 != 0, items the 2-D path repacks
+             (r(4, 96, 256), r(4, 256, 100)),                      # [K, N] B, N % 8 != 0
              (r(0, 8, 64), r(0, 64, 8)), (r(2, 8, 0), r(2, 0, 8))]
     for A, B in cases:
         out = kernels.get("matmul")(A.to(gpu), B.to(gpu)).cpu()
