@@ -305,6 +305,21 @@ def test_matmul_misaligned_operands_repacked(gpu, M, N, K, layout, dt):
     assert torch.equal(out, direct), f"repacked != element-load kernel {M}x{N}x{K} {layout} {dt}"
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
+def test_matmul_batched_past_grid_z_limit(gpu, dt):
+    """70000 items: past the 65535 a grid's z dimension holds, so ak_gemm_batched runs the batch in
+    two chunks; every item against the oracle, including the first and last of each chunk."""
+    g = torch.Generator().manual_seed(5)
+    A = (torch.randn(70000, 8, 16, generator=g) / 4).to(dt)
+    B = torch.randn(70000, 16, 24, generator=g).to(dt)
+    out = kernels.get("matmul")(A.to(gpu), B.to(gpu)).cpu()
+    exp = R.matmul_ref(A.float(), B.float()).to(dt)
+    tol = 1e-4 if dt == torch.float32 else 2e-2
+    assert_close(out, exp, tol, tol, f"70000 x [8 x 24 x 16] {dt}")
+    for i in (0, 65534, 65535, 69999):
+        assert_close(out[i], exp[i], tol, tol, f"item {i} {dt}")
+
+
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
 def test_matmul_batched_one_launch(gpu, dt):
     """torch.matmul's batched and broadcast forms run as one ak_gemm_batched launch (the batch on the
