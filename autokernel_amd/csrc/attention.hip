@@ -349,15 +349,16 @@ __device__ __forceinline__ u32x4 fa2_rsrc(const void* base, uint32_t nbytes) {
 }
 
 // One 1 KB LDS-DMA transfer: lane L's 16 bytes from rsrc + voff land at LDS byte lds + 16 L.
-// Inline assembly, so the compiler inserts no waits for it: every wait is an explicit vmcnt.
+// Inline assembly, so the compiler inserts no waits for it: every wait is an explicit vmcnt. The
+// LDS destination is an input operand bound to M0 ("{m0}"): the compiler writes M0 itself, so no
+// register changes behind its back. One wait state separates the M0 write from the load.
 __device__ __forceinline__ void fa2_dma16(const u32x4& rsrc, uint32_t voff, uint32_t lds) {
   asm volatile(
-      "s_mov_b32 m0, %2\n\t"
       "s_nop 0\n\t"
       "buffer_load_dwordx4 %0, %1, 0 offen lds"
       :
-      : "v"(voff), "s"(rsrc), "s"(lds)
-      : "memory", "m0");
+      : "v"(voff), "s"(rsrc), "{m0}"(lds)
+      : "memory");
 }
 
 typedef short fa2_s16x4 __attribute__((ext_vector_type(4)));

@@ -542,16 +542,17 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma(
 // The same transfer as inline assembly. The compiler then does not track it: its wait-count pass
 // inserts no waits for it (a conservative full wait at a loop head otherwise drains the whole
 // four-stage pipeline once per iteration), and every wait is the caller's explicit vmcnt. M0
-// holds the wave-uniform LDS destination; one wait state separates its write from the load.
+// holds the wave-uniform LDS destination. It is an input operand bound to M0 ("{m0}"), so the
+// compiler writes M0 itself and knows its value; the statement changes no register behind the
+// compiler's back. One wait state separates the M0 write from the load.
 __device__ __forceinline__ void dma16_asm(const char* base, uint32_t off, uint16_t* lds_row_base) {
   const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)lds_row_base;
   asm volatile(
-      "s_mov_b32 m0, %2\n\t"
       "s_nop 0\n\t"
       "global_load_lds_dwordx4 %0, %1"
       :
-      : "v"(off), "s"(base), "s"(lds)
-      : "memory", "m0");
+      : "v"(off), "s"(base), "{m0}"(lds)
+      : "memory");
 }
 
 // Multi-stage variant: NS LDS stages of BKD-deep tiles (BKD 64: 128-byte rows, chunk c of row r

@@ -369,7 +369,10 @@ __global__ __launch_bounds__(kWideThreads) void softmax_wide(const typename T::S
 // of a dword (odd widths put every other row there). The element left at either end (the first
 // when par = 1, the last when cols - par is odd) is one extra value held by thread 0 (first) or 1
 // (last). Pairs past the row's end come back as zeros from the buffer's range check and are
-// masked by index. Requires the output rows to share the input rows' dword alignment.
+// masked by index. The whole byte offset of a load is its VGPR offset: on gfx9 the range check
+// covers the VGPR and instruction offsets, not the scalar offset, so a per-k scalar offset would let
+// reads run past the row (and, on a tensor's last row, past its allocation). Requires the output
+// rows to share the input rows' dword alignment.
 template <typename T, int NP>
 struct WidePairs {
   uint32_t p[NP];
@@ -388,7 +391,7 @@ struct WidePairs {
     const __amdgpu_buffer_rsrc_t r = row_rsrc(row + par, npairs * 4);
 #pragma unroll
     for (int k = 0; k < NP; ++k)
-      p[k] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)threadIdx.x * 4, k * kWideThreads * 4, 0);
+      p[k] = __builtin_amdgcn_raw_buffer_load_b32(r, ((int)threadIdx.x + k * kWideThreads) * 4, 0, 0);
     has_xt = (threadIdx.x == 0 && par) || (threadIdx.x == 1 && ((cols - par) & 1));
     xt = has_xt ? T::to_f(row[threadIdx.x == 0 ? 0 : cols - 1]) : -INFINITY;
     float m = xt;
@@ -459,7 +462,7 @@ __device__ __forceinline__ void stream_ms(const uint16_t* xr, int cols, float* r
     uint32_t p[kStreamUnroll];
 #pragma unroll
     for (int u = 0; u < kStreamUnroll; ++u)
-      p[u] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)threadIdx.x * 4, (b + u * kLoopThreads) * 4, 0);
+      p[u] = __builtin_amdgcn_raw_buffer_load_b32(r, ((int)threadIdx.x + b + u * kLoopThreads) * 4, 0, 0);
     float cm = -INFINITY;
 #pragma unroll
     for (int u = 0; u < kStreamUnroll; ++u)
@@ -506,7 +509,7 @@ __global__ __launch_bounds__(kLoopThreads) void softmax_stream(const uint16_t* _
     uint32_t p[kStreamUnroll];
 #pragma unroll
     for (int u = 0; u < kStreamUnroll; ++u)
-      p[u] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)threadIdx.x * 4, (b + u * kLoopThreads) * 4, 0);
+      p[u] = __builtin_amdgcn_raw_buffer_load_b32(r, ((int)threadIdx.x + b + u * kLoopThreads) * 4, 0, 0);
 #pragma unroll
     for (int u = 0; u < kStreamUnroll; ++u)
       if (b + u * kLoopThreads + (int)threadIdx.x < npairs) {
