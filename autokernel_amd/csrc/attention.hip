@@ -29,6 +29,10 @@
 namespace ak {
 
 constexpr int kFaBKV = 64;   // keys per tile
+// fa_fwd2's lazy exp2 base: a row's base is raised only when a tile's max passes it by more than
+// this (log2 units), so P <= 2^8 (exact range in f16 / bf16) and, after a row's first tile, the
+// O rescale is almost never needed.
+constexpr float kFa2Slack = 8.0f;
 
 constexpr int kFaWaves = 4;                  // waves per block, 32 query rows each
 constexpr int kFaBQ = 32 * kFaWaves;         // query rows per block
@@ -314,10 +318,14 @@ __global__ __launch_bounds__(kFaThreads, 8 / kFaWaves) void fa_fwd(
 //     some unmasked score reaches the overflow threshold (an inf score) or when every unmasked
 //     score is at or below minus the threshold (a row of -inf); both are decided once per row from
 //     the true row max.
-//   * Rounding as stock SDPA does it: the exp2 base is the exact running max, so P <= 1 is rounded
-//     to f16 / bf16 for the P V product; row sums add the unrounded fp32 P; O is scaled by the
-//     reciprocal of the row sum at the end. (A lazily raised base rounds P at other points; measured against SDPA,
-//     this arithmetic agrees bit for bit on 97 % of outputs, the lazy base on 59 %.)
+//   * Lazy exp2 base: a row's base is raised only when a tile's max passes it by more than
+//     kFa2Slack (log2 units), so P <= 2^8 is rounded to f16 / bf16 for the P V product and the row
+//     sums add those rounded values (v_dot2 against ones: the weights that multiply V are the ones
+//     normalised). Past a row's first tile the base almost never moves, so the O rescale sits
+//     behind a wave-uniform branch after phase 2 instead of 64 multiplies per tile. Measured against
+//     the exact running max (P <= 1, unrounded fp32 row sums: SDPA's rounding, 99.8 % bit-equal to
+//     it), one process, f16: [1, 32, 8192, 128] 576.7 -> 549.5 us, [4, 32, 2048, 128] 183.3 ->
+//     181.5 us, [1, 32/8, 2048, 128] 61.2 -> 57.8 us.
 // LDS swizzles (16-byte chunk c of row r):
 //   K: c ^ (r & 15) for D = 128, c ^ ((r >> 1) & 7) for D = 64. gfx950 serves a ds_read_b128 in
 //      16-lane phases (256 bytes); the 16 lanes of a phase read rows r..r+15 at one chunk.
@@ -379,6 +387,20 @@ __device__ __forceinline__ uint32_t fa2_pack<TBF16>(float a, float b) {
   typedef float f2 __attribute__((ext_vector_type(2)));
   typedef __bf16 b2 __attribute__((ext_vector_type(2)));
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, b2));
+}
+// acc + p.lo + p.hi (p: two packed values)
+template <typename T>
+__device__ __forceinline__ float fa2_sum2(uint32_t p, float acc);
+template <>
+__device__ __forceinline__ float fa2_sum2<TF16>(uint32_t p, float acc) {
+  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p), one, acc, false);
+}
+template <>
+__device__ __forceinline__ float fa2_sum2<TBF16>(uint32_t p, float acc) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const b2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, p), one, acc, false);
 }
 // Keeps the computation of x ahead of this point (an empty use the compiler cannot move).
 __device__ __forceinline__ void fa2_pin(const f32x16& x) { asm volatile("" ::"v"(x)); }
@@ -526,7 +548,7 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   };
 
   float m_run = -INFINITY, l_run = 0.f, m_true = -INFINITY;
-  // row statistics of S_j: mask, tile max (raw units), lazy base update
+  // row statistics of S_j: mask, tile max (raw units), lazy base update (alpha = 1 unless it moved)
   auto stats = [&](f32x16 (&s)[2], int k0, bool masked, float& alpha, float& base) {
     if (masked) {
 #pragma unroll
@@ -551,7 +573,7 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
     mt = fa2_halves_max(mt);
     m_true = fmaxf(m_true, mt);
     const float mts = mt * c_log2;
-    const float m_new = fmaxf(m_run, mts);  // exact running max: P <= 1, as SDPA rounds it
+    const float m_new = (mts > m_run + kFa2Slack || m_run == -INFINITY) ? fmaxf(m_run, mts) : m_run;
     base = (m_new == -INFINITY) ? 0.f : m_new;
     alpha = (m_new == m_run) ? 1.0f : __builtin_amdgcn_exp2f(m_run - base);
     m_run = m_new;
@@ -575,8 +597,7 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
         const float x0 = __builtin_amdgcn_exp2f(s[t >> 1][v]);
         const float x1 = __builtin_amdgcn_exp2f(s[t >> 1][v + 1]);
         pf[t][e] = fa2_pack<T>(x0, x1);
-        ps += x0;
-        ps += x1;
+        ps = fa2_sum2<T>(pf[t][e], ps);
       }
     return ps;
   };
@@ -638,9 +659,9 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   // branch between them, so the MFMAs of one part and the VALU work of the other share one block.
   auto iter_fast = [&](int j, int par, f32x16 (&S)[2], f32x16 (&Sn)[2]) {
     // phase 1: O^T += V_{j-1}^T P_{j-1}^T beside the row max of S_j and its exponent arguments
-    // (pinned here, so that phase 2 holds only the exponentials, the packing, the row sums and the
-    // rescale). Nothing in this phase waits on VALU results, so one MFMA, two fragment reads and five
-    // VALU instructions interleave throughout; fragment reads run one MFMA ahead of their use.
+    // (pinned here, so that phase 2 holds only the exponentials, the packing and the row sums).
+    // Nothing in this phase waits on VALU results, so one MFMA, two fragment reads and four VALU
+    // instructions interleave throughout; fragment reads run one MFMA ahead of their use.
     pv(sV + (par ^ 1) * TILE);
     float alpha, base;
     stats(S, j * kFaBKV, false, alpha, base);
@@ -652,44 +673,42 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
     for (int i = 0; i < 14; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the V^T fragment of MFMA i + 2
-      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // 5 VALU
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     sync_mid(j, par);
-    // phase 2: S_{j+1} = K_{j+1} Q^T beside P_j = exp2(...), its row sum and O^T <- alpha_j O^T
-    // (O^T is not touched by this phase's MFMAs). The rescale is unconditional: a branch around it
-    // duplicates the block and costs more in register moves than it saves.
+    // phase 2: S_{j+1} = K_{j+1} Q^T beside P_j = exp2(...) and its row sum
     qk(sK + (par ^ 1) * TILE, Sn);
     const float ps = exp_pack(S);
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
-    // keep P_j's computation and the rescale here (otherwise they sink to their first use after the
-    // barrier)
+    // keep P_j's computation here (otherwise it sinks to its first use after the barrier)
 #pragma unroll
     for (int t = 0; t < 4; ++t) asm volatile("" ::"v"(pf[t]));
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) fa2_pin(o[db]);
     asm volatile("" ::"v"(ps));
     __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
 #pragma unroll
     for (int i = 0; i < 14; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // 1 MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);  // the K fragment of MFMA i + 2
-      __builtin_amdgcn_sched_group_barrier(0x402, 9, 1);  // 9 VALU / transcendental
+      __builtin_amdgcn_sched_group_barrier(0x402, 5, 1);  // 5 VALU / transcendental
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x402, 9, 1);
+      __builtin_amdgcn_sched_group_barrier(0x402, 5, 1);
     }
     __builtin_amdgcn_sched_barrier(0);
+    // O^T <- alpha_j O^T (O^T is not touched by phase 2's MFMAs), only when some row's base moved
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+    }
     l_run = l_run * alpha + ps;
     sync_end(j, par);
   };

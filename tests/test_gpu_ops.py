@@ -156,35 +156,37 @@ def test_baseline_fused_mlp(gpu):
 
 @pytest.mark.parametrize("B,S", [(4, 2048), (1, 8192)])
 def test_baseline_attention(gpu, B, S):
-    """C4 at full size. The oracle materialises S x S scores per (batch, head), so it runs one head
-    at a time: every (batch, head) pair at S = 2048, eight heads spread over 0..31 (the last
-    included) at S = 8192, where one head costs about a second of CPU."""
+    """C4 at full size, every (batch, head) pair at both shapes. The oracle materialises S x S
+    scores per (batch, head), so it runs one head at a time (about a second of CPU per head at
+    S = 8192)."""
     i = spec.baseline_attention(B=B, S=S)
     out = kernels.get("flash_attention")(**to_dev(i, gpu)).cpu()
-    heads = range(32) if S <= 2048 else (0, 5, 10, 15, 20, 25, 28, 31)
     for b in range(B):
-        for h in heads:
+        for h in range(32):
             sl = (slice(b, b + 1), slice(h, h + 1))
             exp = R.flash_attention_ref(i["Q"][sl], i["K"][sl], i["V"][sl])
             assert_close(out[sl], exp, 1e-2, 1e-2, f"C4 attention B{B} S{S} batch {b} head {h}")
 
 
-@pytest.mark.parametrize("dt,floor", [(torch.float16, 0.995), (torch.bfloat16, 0.999)])
-def test_attention_rounds_like_sdpa(gpu, dt, floor):
-    """The flash kernel's arithmetic (P against the exact running max, rounded for the P V product,
-    unrounded fp32 row sums, one reciprocal at the end, 64-key tiles) reproduces the image's stock
-    SDPA kernel bit for bit on almost every output: measured 99.77 % (f16) and 99.97 % (bf16) at the
-    7B forward's [1, 32, 2048, 128]; the rest differ in fp32 summation order. A change to that
-    arithmetic shows here first. Inputs as C4 (N(0, 1), seeded on the CPU)."""
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_attention_as_accurate_as_sdpa(gpu, dt):
+    """The flash kernel's arithmetic (a lazily raised exp2 base, P rounded for the P V product, row
+    sums of the rounded P, one reciprocal at the end) is as accurate as the image's stock SDPA: at
+    the 7B forward's [1, 32, 2048, 128], causal, its mean distance to an fp32 evaluation of the same
+    inputs is within 10 % of SDPA's and its largest within 50 % (measured: mean +3.9 % in f16 and
+    bf16, max 8 % / 24 % below SDPA's). Inputs as C4 (N(0, 1), seeded on the CPU); the fp32
+    reference is SDPA on the fp32 copies."""
     g = torch.Generator().manual_seed(7)
     q, k, v = (torch.randn(1, 32, 2048, 128, generator=g).to(dt).to(gpu) for _ in range(3))
-    out = kernels.get("flash_attention")(q, k, v, causal=True)
-    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True)
-    same = (out == ref).float().mean().item()
-    diff = (out.float() - ref.float()).abs().max().item()
-    print(f"attention {dt}: {100 * same:.3f} % bit-equal to stock SDPA, max |d| {diff:.3e}", flush=True)
-    assert same >= floor, (dt, same)
-    assert diff <= (4e-3 if dt == torch.float16 else 2e-2), (dt, diff)
+    out = kernels.get("flash_attention")(q, k, v, causal=True).float()
+    sdpa = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True).float()
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True)
+    e_ak, e_sdpa = (out - ref).abs(), (sdpa - ref).abs()
+    same = (out == sdpa).float().mean().item()
+    print(f"attention {dt}: vs fp32 mean {e_ak.mean().item():.3e} max {e_ak.max().item():.3e}; stock SDPA mean "
+          f"{e_sdpa.mean().item():.3e} max {e_sdpa.max().item():.3e}; {100 * same:.2f} % bit-equal to SDPA", flush=True)
+    assert e_ak.mean() <= 1.10 * e_sdpa.mean(), (dt, e_ak.mean().item(), e_sdpa.mean().item())
+    assert e_ak.max() <= 1.5 * e_sdpa.max(), (dt, e_ak.max().item(), e_sdpa.max().item())
 
 
 # ----------------------------------------------------------------------- golden fixtures
