@@ -24,6 +24,6 @@ extern "C" int ak_copy(const void* src, void* dst, int64_t bytes, hipStream_t st
   if (bytes % 16 != 0 || !host_aligned16(src) || !host_aligned16(dst)) return AK_EUNSUPPORTED;
   const int64_t n = bytes / 16, nb = cdiv(n, 256);
   if (nb > INT_MAX) return AK_EINVAL;
-  copy16<<<(unsigned)nb, 256, 0, stream>>>((const u32x4*)src, (u32x4*)dst, n);
+  launch_timed(copy16, dim3((unsigned)nb), dim3(256), 0, stream, (const u32x4*)src, (u32x4*)dst, n);
   return record_launch();
 }

@@ -545,12 +545,14 @@ static int launch_softmax(const void* x, void* y, int64_t rows, int64_t cols, hi
   RowPlan plan;
   const bool vec = cols % T::kVec == 0 && host_aligned16(x) && host_aligned16(y);
   bool handled = false;
-  // An output of 64 MiB or more is stored nontemporally: back to back (the benchmark's steady
-  // state), dirty cache lines left by plain stores are written back during the next kernel.
-  // Measured, f16 [8192, 8192] in a loop with RoPE: 50.4 -> 43.1 us per softmax. (Timed alone
-  // after a cache flush, plain stores look faster, 43.4 against 48.2 us: their write-back then
-  // lands after the kernel.) Smaller outputs keep plain stores, so a consumer can find them in cache.
-  const int nt_out = rows * cols * (int64_t)sizeof(S) >= ((int64_t)64 << 20);
+  // An output larger than the 256 MB Infinity Cache is stored nontemporally; smaller outputs keep
+  // plain stores, so the consumer that usually reads them next finds them in cache. Measured, f16
+  // [8192, 8192] (128 MiB), cold, softmax then a consumer of its output: with a reduce sum 62.9 us
+  // plain against 69.7 us nontemporal, with a [8192, 8192] x [8192, 128] product 88.2 against
+  // 89.5 us. Nontemporal stores win only for back-to-back softmax calls whose outputs nobody reads
+  // (the dirty lines' write-back then lands in the next kernel): 56.3 against 67.3 us per
+  // RoPE(q), RoPE(k), softmax step.
+  const int nt_out = rows * cols * (int64_t)sizeof(S) > ((int64_t)256 << 20);
   if (vec && plan_row(cols / T::kVec, T::kVec, &plan)) {
     AK_ROW_SWITCH({
       const dim3 grid((unsigned)cdiv(rows, RowGeom<L>::kRowsPerBlock));
