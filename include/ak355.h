@@ -54,7 +54,7 @@ const char* ak_status_string(int status);
 const char* ak_last_hip_error_string(void);
 
 /*
- * Measurement hook: the calling thread's next timed launch (currently ak_softmax) records `start`
+ * Measurement hook: the calling thread's next timed launch (ak_softmax, ak_copy) records `start`
  * and `stop` (created HIP events, or NULL) as part of its kernel dispatch, at the kernel's start
  * and end, through hipExtLaunchKernel; the setting is then cleared. Event pairs recorded this way
  * time the kernel alone, without the gap a separate hipEventRecord leaves before the dispatch.
@@ -265,7 +265,7 @@ int ak_gemm_rope(int dtype, const void* A, const void* B, void* C, int64_t M, in
 /*
  * Device copy of `bytes` bytes (a multiple of 16, 16-byte aligned src and dst), one 16-byte vector
  * per thread. No counterpart in the reference: the bandwidth reference the benchmark times beside
- * the HBM-bound ops (the practical ceiling at a given size).
+ * the HBM-bound ops (the practical ceiling at a given size). A timed launch (ak_set_launch_events).
  */
 int ak_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream);
 
