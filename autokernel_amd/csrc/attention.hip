@@ -657,10 +657,17 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   };
   // Steady-state iteration (1 <= j, tile j unmasked, j + 1 <= jw): all four parts run, with no
   // branch between them, so the MFMAs of one part and the VALU work of the other share one block.
+  // Interleave pattern of the steady state: each phase has D / 8 MFMAs (16 at D = 128, 8 at D = 64)
+  // beside about the same softmax work, so the VALU instructions per MFMA follow D (measured at
+  // D = 64 against the D = 128 pattern: [1, 32, 4096, 64] 104.7 -> 103.4 us, [2, 32, 2048, 64]
+  // 62.6 -> 61.2 us, smaller shapes within 1 %).
+  constexpr int kPhaseMfma = D / 8;
+  constexpr int kP1Valu = D == 128 ? 4 : 8;
+  constexpr int kP2Valu = D == 128 ? 5 : 9;
   auto iter_fast = [&](int j, int par, f32x16 (&S)[2], f32x16 (&Sn)[2]) {
     // phase 1: O^T += V_{j-1}^T P_{j-1}^T beside the row max of S_j and its exponent arguments
     // (pinned here, so that phase 2 holds only the exponentials, the packing and the row sums).
-    // Nothing in this phase waits on VALU results, so one MFMA, two fragment reads and four VALU
+    // Nothing in this phase waits on VALU results, so one MFMA, two fragment reads and kP1Valu VALU
     // instructions interleave throughout; fragment reads run one MFMA ahead of their use.
     pv(sV + (par ^ 1) * TILE);
     float alpha, base;
@@ -670,15 +677,15 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
     for (int kb = 0; kb < 2; ++kb) asm volatile("" ::"v"(S[kb]));
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int i = 0; i < 14; ++i) {
+    for (int i = 0; i < kPhaseMfma - 2; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the V^T fragment of MFMA i + 2
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
+      __builtin_amdgcn_sched_group_barrier(0x002, kP1Valu, 0);
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, kP1Valu, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     sync_mid(j, par);
@@ -691,15 +698,15 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
     asm volatile("" ::"v"(ps));
     __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
 #pragma unroll
-    for (int i = 0; i < 14; ++i) {
+    for (int i = 0; i < kPhaseMfma - 2; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // 1 MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);  // the K fragment of MFMA i + 2
-      __builtin_amdgcn_sched_group_barrier(0x402, 5, 1);  // 5 VALU / transcendental
+      __builtin_amdgcn_sched_group_barrier(0x402, kP2Valu, 1);  // VALU / transcendental
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x402, 5, 1);
+      __builtin_amdgcn_sched_group_barrier(0x402, kP2Valu, 1);
     }
     __builtin_amdgcn_sched_barrier(0);
     // O^T <- alpha_j O^T (O^T is not touched by phase 2's MFMAs), only when some row's base moved
