@@ -478,6 +478,31 @@ def test_attention_gqa_strided(gpu, D, causal):
     assert_close(out, exp, 1e-2, 1e-2, f"GQA D{D} causal={causal}")
 
 
+@pytest.mark.parametrize("D,dt", [(64, torch.float16), (128, torch.float16), (128, torch.bfloat16)])
+@pytest.mark.parametrize("trend", ["rising", "falling"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_moving_row_max(gpu, D, dt, trend, causal):
+    """Scores that rise (or fall) steadily along the key axis: about 5.4 log2 units per 64-key tile
+    over 1024 keys, so with a rising trend every row's maximum passes the kernel's lazily raised
+    exp2 base (slack 8) on every other tile and the O rescale and row-sum update run all through the
+    steady state; with a falling trend they never run after the first tile. Raw Q K^T reaches ~700,
+    where f16 steps are 0.5: the reference's rounding of Q K^T to f16 would itself move these
+    softmax weights by ~3 %, so the expected output is the oracle's op sequence on fp32 copies of
+    the inputs (no intermediate rounding), at the harness's tolerance for the output type."""
+    g = torch.Generator().manual_seed(11 + D)
+    B, H, S = 1, 4, 1024
+    u = torch.randn(D, generator=g)
+    u = u / u.norm()
+    ramp = torch.linspace(0.0, 85.0, S) if trend == "rising" else torch.linspace(85.0, 0.0, S)
+    Q = (8.0 * u + 0.1 * torch.randn(B, H, S, D, generator=g)).to(dt)
+    K = (ramp[:, None] * u + 0.1 * torch.randn(B, H, S, D, generator=g)).to(dt)
+    V = torch.randn(B, H, S, D, generator=g).to(dt)
+    out = kernels.get("flash_attention")(Q.to(gpu), K.to(gpu), V.to(gpu), causal)
+    exp = R.flash_attention_ref(Q.float(), K.float(), V.float(), causal)
+    tol = 1e-2 if dt == torch.float16 else 2e-2
+    assert_close(out, exp, tol, tol, f"{trend} scores D{D} {dt} causal={causal}")
+
+
 def test_attention_rectangular_and_scale(gpu):
     g = torch.Generator().manual_seed(6)
     Q = torch.randn(1, 4, 96, 64, generator=g).bfloat16()
