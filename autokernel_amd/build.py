@@ -54,6 +54,10 @@ def _compile(src: Path, extra: list[str]) -> tuple[Path, str]:
     # keep only real diagnostics (drop the expected host-pass feature warning)
     noise = "is not a recognized feature for this target"
     msgs = "\n".join(l for l in (proc.stderr or "").splitlines() if noise not in l)
+    # inline assembly must not write a register the compiler reserves (M0 is an asm input bound with
+    # "{m0}" instead): such a clobber is not preserved and its value may be live across the statement
+    if "clobber list contains reserved registers" in msgs:
+        raise RuntimeError(f"{src.name}: inline asm clobbers a reserved register:\n{msgs[:2000]}")
     return obj, msgs
 
 
