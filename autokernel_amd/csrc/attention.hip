@@ -551,12 +551,16 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   // row statistics of S_j: mask, tile max (raw units), lazy base update (alpha = 1 unless it moved)
   auto stats = [&](f32x16 (&s)[2], int k0, bool masked, float& alpha, float& base) {
     if (masked) {
+      // key k0 + hh * 4 + off is masked when it is at or past lim (Sk, or my_q + 1 when causal):
+      // one compare against the compile-time offset per score
+      const int lim = causal ? min(Sk, my_q + 1) : Sk;
+      const int t = lim - (k0 + hh * 4);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int key = k0 + kb * 32 + (v >> 2) * 8 + hh * 4 + (v & 3);
-          if (key >= Sk || (causal && key > my_q)) s[kb][v] = -INFINITY;
+          const int off = kb * 32 + (v >> 2) * 8 + (v & 3);
+          if (off >= t) s[kb][v] = -INFINITY;
         }
     }
     // four independent max3 chains over the 32 scores, then one combine
@@ -648,10 +652,12 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
       exp_args(S, base);
       const float ps = exp_pack(S);
       l_run = l_run * alpha + ps;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
+        for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+          for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+      }
     }
     sync_end(j, par);
   };
