@@ -405,9 +405,14 @@ __device__ __forceinline__ float fa2_sum2<TBF16>(uint32_t p, float acc) {
 // Keeps the computation of x ahead of this point (an empty use the compiler cannot move).
 __device__ __forceinline__ void fa2_pin(const f32x16& x) { asm volatile("" ::"v"(x)); }
 // max over the two 32-lane halves (every lane gets the same value, combined in the same order)
+// NaN-propagating max (v_maximum3_f32 / v_maximum_f32). fmaxf would ignore a NaN score, and on
+// MFMA results the compiler then quiets each operand first (one v_max_f32 per operand: 11 more
+// instructions per 64-key tile). A row whose scores hold a NaN comes out NaN either way: its true
+// max fails the overflow test below.
+__device__ __forceinline__ float fa2_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 __device__ __forceinline__ float fa2_halves_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return fa2_max(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float fa2_halves_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -563,19 +568,22 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
           if (off >= t) s[kb][v] = -INFINITY;
         }
     }
-    // four independent max3 chains over the 32 scores, then one combine
+    // four independent max3 chains over 7 scores each, then one max3 chain over their results and
+    // the four scores left (16 three-input maxima for 32 scores)
     float m4[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int kb = c >> 1, v0 = (c & 1) * 8;
-      float m = fmaxf(fmaxf(s[kb][v0], s[kb][v0 + 1]), s[kb][v0 + 2]);
-      m = fmaxf(fmaxf(m, s[kb][v0 + 3]), s[kb][v0 + 4]);
-      m = fmaxf(fmaxf(m, s[kb][v0 + 5]), s[kb][v0 + 6]);
-      m4[c] = fmaxf(m, s[kb][v0 + 7]);
+      float m = fa2_max(fa2_max(s[kb][v0], s[kb][v0 + 1]), s[kb][v0 + 2]);
+      m = fa2_max(fa2_max(m, s[kb][v0 + 3]), s[kb][v0 + 4]);
+      m4[c] = fa2_max(fa2_max(m, s[kb][v0 + 5]), s[kb][v0 + 6]);
     }
-    float mt = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+    float mt = fa2_max(fa2_max(m4[0], s[0][7]), m4[1]);
+    mt = fa2_max(fa2_max(mt, s[0][15]), m4[2]);
+    mt = fa2_max(fa2_max(mt, s[1][7]), m4[3]);
+    mt = fa2_max(mt, s[1][15]);
     mt = fa2_halves_max(mt);
-    m_true = fmaxf(m_true, mt);
+    m_true = fa2_max(m_true, mt);
     const float mts = mt * c_log2;
     const float m_new = (mts > m_run + kFa2Slack || m_run == -INFINITY) ? fmaxf(m_run, mts) : m_run;
     base = (m_new == -INFINITY) ? 0.f : m_new;
