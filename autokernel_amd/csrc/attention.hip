@@ -425,13 +425,19 @@ constexpr int kFa2BQ = 32 * kFa2Waves;
 constexpr int kFa2Threads = 64 * kFa2Waves;
 constexpr int kFa2Layer = 256;  // blocks per layer: one per MI355X compute unit
 
-template <typename T, int D>
-__global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
+// NH = 2 (grids of at most one block per CU): a block is 8 waves, and waves 4..7 take the second
+// half of the block's key tiles for the same 128 queries, in LDS stages of their own. Every wave
+// runs the same number of iterations (the first half's tile count) with two barriers each, so the
+// halves meet at every barrier; the DMA issue and wait counts follow each half's real tile count,
+// so no transfer reads past the block's last key. At the end the second half hands its O^T, exp2
+// base, row sums and true row max to the first through LDS, which combines them and stores O.
+template <typename T, int D, int NH>
+__global__ __launch_bounds__(kFa2Threads * NH, NH == 1 ? 8 / kFa2Waves : 1) void fa_fwd2(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, int Hq, int group, int Sq, int Sk, int64_t qsb, int64_t qsh,
     int64_t qss, int64_t ksb, int64_t ksh, int kss, int64_t vsb, int64_t vsh, int vss,
     int64_t osb, int64_t osh, int64_t oss, int causal, float c_log2, float thr, int nbh) {
-  static_assert((kFa2Waves == 4 || kFa2Waves == 8) && kFaBKV == 64, "fa_fwd2 tiling");
+  static_assert((kFa2Waves == 4 || kFa2Waves == 8) && kFaBKV == 64 && (NH == 1 || NH == 2), "fa_fwd2 tiling");
   constexpr int DC = D / 8;             // 16-byte chunks per row
   constexpr int RPI = 64 / DC;          // rows per 1 KB DMA transfer
   constexpr int NIW = kFaBKV / RPI / kFa2Waves;  // transfers per wave per tile, per matrix
@@ -439,8 +445,8 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   constexpr int NDB = D / 32;           // 32-row d blocks of O^T
   constexpr int TILE = kFaBKV * D;      // elements of one K or V tile
   static_assert(NIW * RPI * kFa2Waves == kFaBKV, "tile rows split over waves");
-  __shared__ __attribute__((aligned(1024))) uint16_t sK[2 * TILE];
-  __shared__ __attribute__((aligned(1024))) uint16_t sV[2 * TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t sKa[NH * 2 * TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t sVa[NH * 2 * TILE];
 
   // Causal work order: blocks come heaviest first (greedy balance over many rounds). A grid of at
   // most two layers of kFa2Layer blocks (one block per CU each) reverses its second layer, so the
@@ -458,7 +464,11 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   const int h = bh % Hq, b = bh / Hq;
   const int hk = h / group;
   const int lane = lane_id();
-  const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int wid = __builtin_amdgcn_readfirstlane(wave_id());
+  const int half = NH == 2 ? wid / kFa2Waves : 0;  // key half (wave-uniform)
+  const int w = wid % kFa2Waves;                    // wave within the half: query rows w * 32 ..
+  uint16_t* const sK = sKa + half * 2 * TILE;       // this half's two K stages
+  uint16_t* const sV = sVa + half * 2 * TILE;
   const int l32 = lane & 31, hh = lane >> 5;
   const int q0 = qb * kFa2BQ;
   const int qw0 = q0 + w * 32;
@@ -476,8 +486,14 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
     qf[s] = (my_q < Sq) ? ld16(Qb + (int64_t)my_q * qss + s * 16 + hh * 8) : u32x4{0u, 0u, 0u, 0u};
 
   const int kend = causal ? min(Sk, q0 + kFa2BQ) : Sk;
-  const int nt = (kend + kFaBKV - 1) / kFaBKV;           // >= 1
-  const int jw = causal ? min(nt - 1, (qw0 + 31) / kFaBKV) : nt - 1;  // this wave's last tile
+  const int ntb = (kend + kFaBKV - 1) / kFaBKV;          // the block's key tiles, >= 1 (>= 2 when NH = 2)
+  // This half's tiles are jbase + 0 .. jbase + nt - 1 (nt >= 1); j below is relative to jbase.
+  // Every wave iterates ntl times: the second half's last iteration is empty when ntb is odd.
+  const int ntl = NH == 2 ? (ntb + 1) / 2 : ntb;
+  const int jbase = half * ntl;
+  const int nt = NH == 2 ? (half ? ntb - ntl : ntl) : ntb;
+  // this wave's last tile in this half (negative when every key of the half is past its queries)
+  const int jw = min(nt - 1, (causal ? min(ntb - 1, (qw0 + 31) / kFaBKV) : ntb - 1) - jbase);
 
   // Per-lane byte offsets of the DMA transfers inside a tile (the tile base is in the resource):
   // transfer n = i * 4 + w covers tile rows n * RPI ..; lane L writes physical chunk L % DC of row
@@ -494,13 +510,13 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   const uint32_t sV_lds = (uint32_t)(uintptr_t)(lds_void*)sV;
 
   auto issue_k = [&](int j, int stage) {
-    const int k0 = j * kFaBKV;
+    const int k0 = (jbase + j) * kFaBKV;
     const u32x4 rs = fa2_rsrc(Kb + (int64_t)k0 * kss, (uint32_t)(((Sk - 1 - k0) * kss + D) * 2));
 #pragma unroll
     for (int i = 0; i < NIW; ++i) fa2_dma16(rs, offk[i], sK_lds + stage * TILE * 2 + (i * kFa2Waves + w) * 1024);
   };
   auto issue_v = [&](int j, int stage) {
-    const int k0 = j * kFaBKV;
+    const int k0 = (jbase + j) * kFaBKV;
     const u32x4 rs = fa2_rsrc(Vb + (int64_t)k0 * vss, (uint32_t)(((Sk - 1 - k0) * vss + D) * 2));
 #pragma unroll
     for (int i = 0; i < NIW; ++i) fa2_dma16(rs, offv[i], sV_lds + stage * TILE * 2 + (i * kFa2Waves + w) * 1024);
@@ -646,7 +662,7 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   // only where this wave needs it (causal tail, first tile), and diagonal / partial tiles are
   // masked.
   auto iter = [&](int j, int par, f32x16 (&S)[2], f32x16 (&Sn)[2]) {
-    const int k0 = j * kFaBKV;
+    const int k0 = (jbase + j) * kFaBKV;
     if (j > 0 && j - 1 <= jw) pv(sV + (par ^ 1) * TILE);  // V_{j-1}
     float alpha = 1.0f, base = 0.f;
     const bool act = j <= jw;
@@ -685,7 +701,7 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
     // instructions interleave throughout; fragment reads run one MFMA ahead of their use.
     pv(sV + (par ^ 1) * TILE);
     float alpha, base;
-    stats(S, j * kFaBKV, false, alpha, base);
+    stats(S, (jbase + j) * kFaBKV, false, alpha, base);
     exp_args(S, base);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) asm volatile("" ::"v"(S[kb]));
@@ -738,12 +754,12 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
   if (nt > 1) issue_k(1, 1);
   issue_v(0, 0);
   dma_barrier<0>();
-  qk(sK, sa);  // S_0 (jw >= 0 always)
+  qk(sK, sa);  // S_0 (jw >= 0 except for a second-half wave whose queries precede all its keys)
   dma_barrier<0>();
   if (nt > 2) issue_k(2, 0);
   // first masked tile of this wave (diagonal or partial), and the end of the steady range
-  const int jm_s = Sk / kFaBKV;
-  const int jm = causal ? min((qw0 + 1) / kFaBKV, jm_s) : jm_s;
+  const int jm_s = Sk / kFaBKV - jbase;
+  const int jm = causal ? min((qw0 + 1) / kFaBKV - jbase, jm_s) : jm_s;
   const int jf = max(1, min(jm, jw));
   // Register roles are fixed at compile time: S_j is in sb at odd j of the steady loop, in sa
   // at even j; the general iterations always take S_j from sa and leave S_{j+1} in sa.
@@ -760,13 +776,45 @@ __global__ __launch_bounds__(kFa2Threads, 8 / kFa2Waves) void fa_fwd2(
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) sa[kb] = sb[kb];
   }
-  for (; j < nt; ++j) {
+  for (; j < ntl; ++j) {
     iter(j, j & 1, sa, sb);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) sa[kb] = sb[kb];
   }
-  if (nt - 1 <= jw) pv(sV + ((nt - 1) & 1) * TILE);
+  if (ntl - 1 <= jw) pv(sV + ((ntl - 1) & 1) * TILE);
   wait_vmcnt<0>();  // (no transfer is outstanding here; kept so none can outlive the block)
+
+  if constexpr (NH == 2) {
+    // Hand-over: every wave is done with its K / V stages, so they hold the second half's
+    // results, [wave][value][lane] (conflict-free): O^T in the K stages, the three row scalars
+    // in the V stages.
+    dma_barrier<0>();
+    float* xo = reinterpret_cast<float*>(sKa) + w * (NDB * 16) * 64 + lane;
+    float* xs = reinterpret_cast<float*>(sVa) + w * 3 * 64 + lane;
+    if (half == 1) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) xo[(db * 16 + v) * 64] = o[db][v];
+      xs[0] = m_run;
+      xs[64] = l_run;
+      xs[128] = m_true;
+    }
+    dma_barrier<0>();
+    if (half == 1) return;
+    // O = (O_0 2^(b_0 - b) + O_1 2^(b_1 - b)) / (l_0 2^(b_0 - b) + l_1 2^(b_1 - b)), b = max(b_0, b_1);
+    // a half with no key for this query has base -inf, O = 0 and l = 0
+    const float m1 = xs[0], l1 = xs[64], t1 = xs[128];
+    const float mb = fmaxf(m_run, m1);
+    const float a0 = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - mb);
+    const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mb);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[db][v] = o[db][v] * a0 + xo[(db * 16 + v) * 64] * a1;
+    l_run = l_run * a0 + l1 * a1;
+    m_true = fa2_max(m_true, t1);
+  }
 
   // ---- epilogue: O[q][d] = O^T[d][q] / l; NaN rows where the reference's scores overflow ----
   // one correctly rounded reciprocal per row, then products (a NaN row multiplies by NaN)
@@ -1029,11 +1077,19 @@ static int launch_fa(const void* Q, const void* K, const void* V, void* O, int64
   // byte offsets; anything else takes fa_fwd.
   const int64_t span = (int64_t)2 * Sk * (ks[2] > vs[2] ? ks[2] : vs[2]);
   if (sm_scale > 0.f && span < ((int64_t)1 << 31) && ks[2] >= D && vs[2] >= D) {
-    fa_fwd2<T, D><<<dim3((unsigned)nblocks2), kFa2Threads, 0, st>>>(
-        (const uint16_t*)Q, (const uint16_t*)K, (const uint16_t*)V, (uint16_t*)O, (int)Hq,
-        (int)(Hq / Hkv), (int)Sq, (int)Sk, qs[0], qs[1], qs[2], ks[0], ks[1], (int)ks[2], vs[0],
-        vs[1], (int)vs[2], os[0], os[1], os[2], causal, sm_scale * kFaLog2e,
-        T::kCode == AK_F16 ? thr : INFINITY, (int)(Hq * B));
+    // A grid of at most one block per CU splits each block's keys over two wave groups (the
+    // block's serial walk over its key tiles bounds such a grid). Sk >= 256 gives every block at
+    // least two key tiles (a causal block's keys reach at least its first 128 queries), so each
+    // half has one.
+#define AK_FA2(NH)                                                                                  \
+  fa_fwd2<T, D, NH><<<dim3((unsigned)nblocks2), kFa2Threads * NH, 0, st>>>(                         \
+      (const uint16_t*)Q, (const uint16_t*)K, (const uint16_t*)V, (uint16_t*)O, (int)Hq,            \
+      (int)(Hq / Hkv), (int)Sq, (int)Sk, qs[0], qs[1], qs[2], ks[0], ks[1], (int)ks[2], vs[0],     \
+      vs[1], (int)vs[2], os[0], os[1], os[2], causal, sm_scale * kFaLog2e,                         \
+      T::kCode == AK_F16 ? thr : INFINITY, (int)(Hq * B))
+    if (nblocks2 <= kFa2Layer && Sk >= 4 * kFaBKV) AK_FA2(2);
+    else AK_FA2(1);
+#undef AK_FA2
     return record_launch();
   }
   fa_fwd<T, D><<<grid, kFaThreads, 0, st>>>(

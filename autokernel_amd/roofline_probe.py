@@ -87,9 +87,9 @@ MFMA_PROBES = [
      2 * 2048 * 4096 * 11008 * 2, "mlp"),
     ("gemm_dma<ak::TBF16, 256, 128, 4, 2, 1, 0", "fused_mlp down bf16 2048x4096 K=11008", 2 * 2048 * 4096 * 11008,
      "mlp"),
-    ("fa_fwd2<ak::TF16, 128>", "flash_attention f16 causal [4,32,2048,128]", 2 * 2 * 4 * 32 * 128 * (2048 * 2049 // 2),
+    ("fa_fwd2<ak::TF16, 128, 1>", "flash_attention f16 causal [4,32,2048,128]", 2 * 2 * 4 * 32 * 128 * (2048 * 2049 // 2),
      "fa2k"),
-    ("fa_fwd2<ak::TF16, 128>", "flash_attention f16 causal [1,32,8192,128]", 2 * 2 * 32 * 128 * (8192 * 8193 // 2),
+    ("fa_fwd2<ak::TF16, 128, 1>", "flash_attention f16 causal [1,32,8192,128]", 2 * 2 * 32 * 128 * (8192 * 8193 // 2),
      "fa8k"),
 ]
 

@@ -503,6 +503,35 @@ def test_attention_moving_row_max(gpu, D, dt, trend, causal):
     assert_close(out, exp, tol, tol, f"{trend} scores D{D} {dt} causal={causal}")
 
 
+@pytest.mark.parametrize("D,dt", [(64, torch.float16), (128, torch.float16), (64, torch.bfloat16), (128, torch.bfloat16)])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("Sq,Sk", [(1024, 1024), (777, 777), (300, 1000), (1000, 300), (256, 256), (1023, 1023)])
+def test_attention_split_keys(gpu, D, dt, causal, Sq, Sk):
+    """Grids of at most 256 query blocks with Sk >= 256 split each block's key tiles over two wave
+    groups and merge (O, base, row sum) at the end. Covered: odd tile counts (an empty last
+    iteration in the second half), a partial last key tile, rectangular causal masks both ways (a
+    second-half wave may have no key for its queries), GQA, D 64 / 128, f16 / bf16. Checked against
+    the oracle at the harness tolerance, and against the unsplit kernel on the same inputs (the
+    heads repeated until the grid passes 256 blocks): within four output ulps (P is rounded relative
+    to each half's own exp2 base, so the two paths may round a few weights differently)."""
+    g = torch.Generator().manual_seed(Sq * 3 + Sk + D)
+    B, Hq, Hk = 1, 4, 2
+    Q = torch.randn(B, Hq, Sq, D, generator=g).to(dt)
+    K = torch.randn(B, Hk, Sk, D, generator=g).to(dt)
+    V = torch.randn(B, Hk, Sk, D, generator=g).to(dt)
+    assert -(-Sq // 128) * Hq * B <= 256 and Sk >= 256  # the split path
+    exp = R.flash_attention_ref(Q, K.repeat_interleave(2, 1), V.repeat_interleave(2, 1), causal)
+    out = kernels.get("flash_attention")(Q.to(gpu), K.to(gpu), V.to(gpu), causal)
+    tol = 1e-2 if dt == torch.float16 else 2e-2
+    assert_close(out, exp, tol, tol, f"split keys {Sq}x{Sk} D{D} {dt} causal={causal}")
+    rep = -(-257 // (-(-Sq // 128) * Hq)) + 1  # enough head copies for more than 256 blocks
+    Qr, Kr, Vr = (t.repeat(1, rep, 1, 1).to(gpu) for t in (Q, K, V))
+    whole = kernels.get("flash_attention")(Qr, Kr, Vr, causal)[:, :Hq].cpu()
+    ulp = 2.0 ** -10 if dt == torch.float16 else 2.0 ** -7
+    d = (out.cpu().float() - whole.float()).abs()
+    assert (d <= 4 * ulp * torch.clamp(whole.float().abs(), min=1.0)).all(), d.max().item()
+
+
 def test_attention_rectangular_and_scale(gpu):
     g = torch.Generator().manual_seed(6)
     Q = torch.randn(1, 4, 96, 64, generator=g).bfloat16()

@@ -20,7 +20,8 @@ NAMES = [
     ("attn_fwd", "flash_attention"),
     ("ck_tile::FmhaFwdKernel<...>", "flash_attention"),
     # libak355
-    ("void ak::fa_fwd2<ak::TF16, 128>(unsigned short const*, unsigned short const*)", "flash_attention"),
+    ("void ak::fa_fwd2<ak::TF16, 128, 1>(unsigned short const*, unsigned short const*)", "flash_attention"),
+    ("void ak::fa_fwd2<ak::TBF16, 64, 2>(unsigned short const*, unsigned short const*)", "flash_attention"),
     ("void ak::gemm_dma<ak::TBF16, 256, 128, 2, 4, 2, 1, 64, 2, false>(unsigned short const*)", "fused_mlp"),
     ("void ak::gemm_dma<ak::TBF16, 256, 256, 2, 4, 1, 0, 64, 2, true>(unsigned short const*)", "matmul"),
     ("void ak::gemm_mfma<ak::TF16, true, true, 256, 128, 2, 4, 2, 1>(unsigned short const*)", "fused_mlp"),
