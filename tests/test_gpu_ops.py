@@ -464,9 +464,10 @@ def test_rope_index_arithmetic(gpu, dt):
 
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("causal", [True, False])
-def test_attention_gqa_strided(gpu, D, causal):
-    g = torch.Generator().manual_seed(5)
-    B, S, Hq, Hkv = 2, 200, 8, 2
+@pytest.mark.parametrize("S", [200, 600])  # 600: the split-key path (80 query blocks, Sk >= 256)
+def test_attention_gqa_strided(gpu, D, causal, S):
+    g = torch.Generator().manual_seed(5 + S)
+    B, Hq, Hkv = 2, 8, 2
     q = torch.randn(B, S, Hq, D, generator=g).half()
     k = torch.randn(B, S, Hkv, D, generator=g).half()
     v = torch.randn(B, S, Hkv, D, generator=g).half()
@@ -475,7 +476,7 @@ def test_attention_gqa_strided(gpu, D, causal):
     rep = Hq // Hkv
     exp = R.flash_attention_ref(q.transpose(1, 2).float(), k.transpose(1, 2).repeat_interleave(rep, 1).float(),
                                 v.transpose(1, 2).repeat_interleave(rep, 1).float(), causal)
-    assert_close(out, exp, 1e-2, 1e-2, f"GQA D{D} causal={causal}")
+    assert_close(out, exp, 1e-2, 1e-2, f"GQA D{D} causal={causal} S={S}")
 
 
 @pytest.mark.parametrize("D,dt", [(64, torch.float16), (128, torch.float16), (128, torch.bfloat16)])
