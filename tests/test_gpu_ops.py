@@ -533,6 +533,25 @@ def test_attention_split_keys(gpu, D, dt, causal, Sq, Sk):
     assert (d <= 4 * ulp * torch.clamp(whole.float().abs(), min=1.0)).all(), d.max().item()
 
 
+@pytest.mark.parametrize("D,dt", [(64, torch.float16), (128, torch.bfloat16)])
+@pytest.mark.parametrize("Sk", [1, 63, 64, 300, 4096])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_decode_shapes(gpu, D, dt, Sk, causal):
+    """One query row against 1 .. 4096 keys (a decode step), GQA 32 / 8: the query block holds one
+    valid row, so three of its four waves (in each key half, where the keys split) have no query.
+    With the top-left causal mask the single query sees key 0 only, so its output is V[0]."""
+    g = torch.Generator().manual_seed(Sk + D)
+    Q = torch.randn(2, 32, 1, D, generator=g).to(dt)
+    K = torch.randn(2, 8, Sk, D, generator=g).to(dt)
+    V = torch.randn(2, 8, Sk, D, generator=g).to(dt)
+    exp = R.flash_attention_ref(Q, K.repeat_interleave(4, 1), V.repeat_interleave(4, 1), causal)
+    out = kernels.get("flash_attention")(Q.to(gpu), K.to(gpu), V.to(gpu), causal).cpu()
+    tol = 1e-2 if dt == torch.float16 else 2e-2
+    assert_close(out, exp, tol, tol, f"decode Sk={Sk} D{D} {dt} causal={causal}")
+    if causal:
+        assert torch.equal(out, V.repeat_interleave(4, 1)[:, :, :1]), "causal decode row is V[0]"
+
+
 def test_attention_rectangular_and_scale(gpu):
     g = torch.Generator().manual_seed(6)
     Q = torch.randn(1, 4, 96, 64, generator=g).bfloat16()
