@@ -695,12 +695,26 @@ __global__ __launch_bounds__(kMeanThreads) void ce_mean(const float* __restrict_
                                                         typename T::S* __restrict__ out,
                                                         int64_t rows, int64_t ignore_index) {
   __shared__ float red[kMeanThreads / kWave];
+  // Thread t adds rows t, t + 1024, t + 2048, ... in that order. Each pass loads eight rows' target
+  // and loss before adding any of them, so the loads overlap (a dependent load per row took 4.2 us
+  // for 4096 rows); the order of the additions is the same either way.
+  constexpr int U = 8;
   float s = 0.f, n = 0.f;
-  for (int64_t r = threadIdx.x; r < rows; r += kMeanThreads) {
-    if (tgt[r] != ignore_index) {
-      s += loss[r];
-      n += 1.f;
+  for (int64_t r0 = threadIdx.x; r0 < rows; r0 += (int64_t)U * kMeanThreads) {
+    int64_t t[U];
+    float l[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t r = r0 + (int64_t)u * kMeanThreads;
+      t[u] = r < rows ? tgt[r] : ignore_index;
+      l[u] = r < rows ? loss[r] : 0.f;
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (t[u] != ignore_index) {
+        s += l[u];
+        n += 1.f;
+      }
   }
   s = group_reduce<kMeanThreads, 0>(s, red);
   n = group_reduce<kMeanThreads, 0>(n, red);
