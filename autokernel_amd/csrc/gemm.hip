@@ -1155,8 +1155,9 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
 }
 
 // K slices for a plain f16 / bf16 GEMM on the LDS-DMA path, 1 when splitting does not pay: the
-// chosen tiling must fill at most half the CUs, each slice keeps at least 256 of K (four 64-deep
-// tiles) and a multiple of 64, and slices stop doubling once tiles x slices would pass the CU count.
+// chosen tiling must fill at most half the CUs, each slice keeps at least 1024 of K (sixteen
+// 64-deep tiles) and a multiple of 64, and slices stop doubling once tiles x slices would pass the
+// CU count.
 static int splitk_slices(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, bool bt) {
   if (M <= 0 || N <= 0 || K <= 0 || N % 4 != 0 || ldc % 4 != 0 || lda % 8 != 0 || ldb % 8 != 0) return 1;
   if (M * lda >= INT_MAX || (bt ? N : K) * ldb >= INT_MAX || M * N * 8 >= INT_MAX) return 1;
