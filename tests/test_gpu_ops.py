@@ -169,24 +169,27 @@ def test_baseline_attention(gpu, B, S):
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
-def test_attention_as_accurate_as_sdpa(gpu, dt):
+@pytest.mark.parametrize("H", [32, 8])  # 8 heads: 128 query blocks, the split-key path
+def test_attention_as_accurate_as_sdpa(gpu, dt, H):
     """The flash kernel's arithmetic (a lazily raised exp2 base, P rounded for the P V product, row
     sums of the rounded P, one reciprocal at the end) is as accurate as the image's stock SDPA: at
     the 7B forward's [1, 32, 2048, 128], causal, its mean distance to an fp32 evaluation of the same
     inputs is within 10 % of SDPA's and its largest within 50 % (measured: mean +3.9 % in f16 and
-    bf16, max 8 % / 24 % below SDPA's). Inputs as C4 (N(0, 1), seeded on the CPU); the fp32
-    reference is SDPA on the fp32 copies."""
+    bf16, max 8 % / 24 % below SDPA's). With 8 heads the grid is small enough for the split-key
+    path (two key halves merged at the end), held to the same bounds (measured: mean +2.5 %,
+    max 1.4 % below SDPA's in f16 and equal in bf16). Inputs as C4 (N(0, 1),
+    seeded on the CPU); the fp32 reference is SDPA on the fp32 copies."""
     g = torch.Generator().manual_seed(7)
-    q, k, v = (torch.randn(1, 32, 2048, 128, generator=g).to(dt).to(gpu) for _ in range(3))
+    q, k, v = (torch.randn(1, H, 2048, 128, generator=g).to(dt).to(gpu) for _ in range(3))
     out = kernels.get("flash_attention")(q, k, v, causal=True).float()
     sdpa = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True).float()
     ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True)
     e_ak, e_sdpa = (out - ref).abs(), (sdpa - ref).abs()
     same = (out == sdpa).float().mean().item()
-    print(f"attention {dt}: vs fp32 mean {e_ak.mean().item():.3e} max {e_ak.max().item():.3e}; stock SDPA mean "
+    print(f"attention {dt} H={H}: vs fp32 mean {e_ak.mean().item():.3e} max {e_ak.max().item():.3e}; stock SDPA mean "
           f"{e_sdpa.mean().item():.3e} max {e_sdpa.max().item():.3e}; {100 * same:.2f} % bit-equal to SDPA", flush=True)
-    assert e_ak.mean() <= 1.10 * e_sdpa.mean(), (dt, e_ak.mean().item(), e_sdpa.mean().item())
-    assert e_ak.max() <= 1.5 * e_sdpa.max(), (dt, e_ak.max().item(), e_sdpa.max().item())
+    assert e_ak.mean() <= 1.10 * e_sdpa.mean(), (dt, H, e_ak.mean().item(), e_sdpa.mean().item())
+    assert e_ak.max() <= 1.5 * e_sdpa.max(), (dt, H, e_ak.max().item(), e_sdpa.max().item())
 
 
 # ----------------------------------------------------------------------- golden fixtures
