@@ -91,6 +91,15 @@ MFMA_PROBES = [
      "fa2k"),
     ("fa_fwd2<ak::TF16, 128, 1>", "flash_attention f16 causal [1,32,8192,128]", 2 * 2 * 32 * 128 * (8192 * 8193 // 2),
      "fa8k"),
+    ("gemm_dma<ak::TBF16, 256, 256, 2, 4, 1, 0, 64, 2, false", "matmul bf16 4096^3 (NT: nn.Linear B, LDS-DMA)",
+     2 * 4096 ** 3, "matmul4knt"),
+    # stock torch.matmul on the same operands (the hipBLASLt kernels this image's library picks)
+    ("Cijk_Ailk_Bljk_BBS_BH_Bias_HA_S_SAV_UserArgs_MT256x256x64", "stock hipBLASLt: matmul bf16 4096^3 NN",
+     2 * 4096 ** 3, "blas4k"),
+    ("Custom_Cijk_Alik_Bljk_BBS_BH_Bias_HA_S_SAV_NTD_SK3_UserArgs_MT256x256x64", "stock hipBLASLt: matmul bf16 4096^3 NT",
+     2 * 4096 ** 3, "blas4knt"),
+    ("Custom_Cijk_Alik_Bljk_BBS_BH_MT256x256x64_MI16x16x1_UserArgs", "stock hipBLASLt: matmul bf16 8192^3 NT",
+     2 * 8192 ** 3, "blas8k"),
 ]
 
 
@@ -114,7 +123,12 @@ def run_mfma() -> None:
     f = spec.baseline_fused_mlp(device=dev)
     a = spec.baseline_attention(device=dev)
     a_long = spec.baseline_attention(device=dev, B=1, S=8192)
+    w4 = torch.randn(4096, 4096, device=dev, generator=g).bfloat16()
     calls = {"matmul4k": lambda: kernels.get("matmul")(m["A"], m["B"]),
+             "matmul4knt": lambda: kernels.get("matmul")(m["A"], w4.t()),
+             "blas4k": lambda: torch.matmul(m["A"], m["B"]),
+             "blas4knt": lambda: torch.matmul(m["A"], w4.t()),
+             "blas8k": lambda: torch.matmul(a8, w8.t()),
              "matmul8k": lambda: kernels.get("matmul")(a8, w8.t()),
              "mlp": lambda: kernels.get("fused_mlp")(**f),
              "fa2k": lambda: kernels.get("flash_attention")(**a),
@@ -262,6 +276,10 @@ MFMA_IDEAL_BYTES = {
     "mlp_down": (2048 * 11008 + 4096 * 11008 + 2048 * 4096) * 2,
     "fa2k": 4 * 4 * 32 * 2048 * 128 * 2,
     "fa8k": 4 * 32 * 8192 * 128 * 2,
+    "matmul4knt": 3 * 4096 * 4096 * 2,
+    "blas4k": 3 * 4096 * 4096 * 2,
+    "blas4knt": 3 * 4096 * 4096 * 2,
+    "blas8k": 3 * 8192 * 8192 * 2,
 }
 
 
@@ -275,7 +293,7 @@ def summarize_mfma_traffic(dirpath: str) -> None:
         vals = [c[ctr] for _, n, c, _ in allrows if ctr in c and ("copy" in n.lower() or "elementwise" in n.lower())
                 and c[ctr] * 1024 > COPY_BYTES / 4]
         cal[ctr] = COPY_BYTES / (1024 * sum(vals) / len(vals)) if vals else 1.0
-    keys = ["matmul4k", "matmul8k", "mlp_gateup", "mlp_down", "fa2k", "fa8k"]
+    keys = ["matmul4k", "matmul8k", "mlp_gateup", "mlp_down", "fa2k", "fa8k", "matmul4knt", "blas4k", "blas4knt", "blas8k"]
     lines = ["# Traffic past L2 of the matrix kernels (rocprofv3 PMC)", "",
              "Commands (one counter group per run):", "",
              "    rocprofv3 --pmc FETCH_SIZE -d DIR -o fetch --output-format csv -- python -m autokernel_amd.roofline_probe run_mfma",
