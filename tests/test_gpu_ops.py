@@ -58,20 +58,29 @@ def test_sweep(gpu, op, label, size, dtype):
     cfg = spec.KERNEL_CONFIGS[op]
     inputs = cfg["input_generator"](size, dtype, "cpu", seed=42)
     expected = R.REFERENCE[op](inputs)
-    out = kernels.get(op)(**to_dev(inputs, gpu))
+    dev_inputs = to_dev(inputs, gpu)
+    out = kernels.get(op)(**dev_inputs)
     torch.cuda.synchronize()
     assert not (has_nan_inf(out) and not has_nan_inf(expected)), f"{op} {label}: NaN/Inf in output"
     tol = cfg["tolerances"][dtype]
     if op == "layernorm" and dtype == torch.bfloat16:
         # The harness's bf16 layernorm tolerance (2e-3) is below one bf16 rounding step (2^-8
         # relative): two fp32 implementations round rare near-tie values to neighbouring bf16
-        # values. Check the north-star bf16 tolerance and that such flips stay rare.
+        # values. Stock F.layer_norm on the GPU misses 2e-3 against the same oracle on about the
+        # same share of elements (measured 0-0.0006 % for both). Check the north-star bf16
+        # tolerance, that such flips stay rare, and that they are no more frequent than stock's.
         assert_close(out, expected, 1e-2, 1e-2, f"{op} {label} {dtype}")
+        bound = tol["atol"] + tol["rtol"] * expected.float().abs()
         d = (out.float().cpu() - expected.float()).abs()
-        flips = (d > tol["atol"] + tol["rtol"] * expected.float().abs()).float().mean().item()
+        flips = (d > bound).float().mean().item()
+        x = dev_inputs["x"]
+        stock = torch.nn.functional.layer_norm(x, x.shape[-1:], dev_inputs["weight"], dev_inputs["bias"], 1e-5)
+        stock_flips = ((stock.float().cpu() - expected.float()).abs() > bound).float().mean().item()
         print(f"layernorm bf16 {label} {tuple(size.values())}: {flips:.4%} of elements beyond the table's "
-              f"{tol['atol']:g} (one bf16 step), max |d| {d.max().item():.3e}", flush=True)
+              f"{tol['atol']:g} (one bf16 step; stock GPU F.layer_norm {stock_flips:.4%}), max |d| "
+              f"{d.max().item():.3e}", flush=True)
         assert flips < 1e-3, f"{op} {label}: {flips:.2%} of elements differ by a bf16 step"
+        assert flips <= 4 * stock_flips + 1e-5, f"{op} {label}: {flips:.4%} flips against stock's {stock_flips:.4%}"
         return
     assert_close(out, expected, tol["atol"], tol["rtol"], f"{op} {label} {dtype}")
 
