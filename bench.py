@@ -28,6 +28,8 @@ Also reported (same JSON line):
                 and the reference harness's primary sizes of layernorm / cross-entropy / reduce,
                 cold-cache timed (cache cleared before each call), vs stock PyTorch-ROCm; first two
                 rows: a device copy of the bytes RoPE and softmax move (the practical ceiling).
+                peak_extra_vram_mb (and torch_...): device memory one call allocates beyond what
+                is live (outputs and temporaries), from the caching allocator's peak.
   e2e           LLaMA-7B-shaped forward [1, 2048] f16, stock PyTorch vs the reference verify's swap
                 set (matmul, rmsnorm), every op but attention, and every op; each timed and compared.
 Progress goes to stderr.
@@ -168,16 +170,30 @@ def op_table():
     K = kernels.get
     rows = []
 
+    def extra_vram_mb(f):
+        """Device memory one call allocates beyond what is already live (its outputs and
+        temporaries), from the caching allocator's peak."""
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        out = f()
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated()
+        del out
+        return round((peak - base) / 2 ** 20, 2)
+
     def add(name, unit, work, fn, ref, note=""):
         t = harness.do_bench(fn)
         tr = harness.do_bench(ref) if ref is not None else None
         rate = work / (t["median"] * 1e-3) / (1e9 if unit == "GB/s" else 1e12)
         peak = HBM_PEAK_GBS if unit == "GB/s" else MFMA_PEAK_TFLOPS
         row = {"op": name, "median_us": round(t["median"] * 1e3, 2), "mean_us": round(t["mean"] * 1e3, 2),
-               "achieved": round(rate, 1), "unit": unit, "peak": peak, "frac": round(rate / peak, 4)}
+               "achieved": round(rate, 1), "unit": unit, "peak": peak, "frac": round(rate / peak, 4),
+               "peak_extra_vram_mb": extra_vram_mb(fn)}
         if tr is not None:
             row["torch_median_us"] = round(tr["median"] * 1e3, 2)
             row["speedup_vs_torch"] = round(tr["median"] / t["median"], 3)
+            row["torch_peak_extra_vram_mb"] = extra_vram_mb(ref)
         if note:
             row["note"] = note
         rows.append(row)
