@@ -316,10 +316,44 @@ def e2e(timed: int = 20, warm: int = 3):
     return res
 
 
+def _graph_timing(run, timed: int):
+    """(output, median ms) of `timed` replays of one forward captured in a HIP graph
+    (torch.cuda.CUDAGraph), warmed up on a side stream first; each replay is event-timed."""
+    import torch
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                run()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = run()
+    if not isinstance(out, torch.Tensor):
+        out = out[0]
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    st = [torch.cuda.Event(enable_timing=True) for _ in range(timed)]
+    en = [torch.cuda.Event(enable_timing=True) for _ in range(timed)]
+    for i in range(timed):
+        st[i].record()
+        g.replay()
+        en[i].record()
+    torch.cuda.synchronize()
+    t = sorted(a.elapsed_time(b) for a, b in zip(st, en))
+    res = out.clone()
+    del g, out
+    return res, t[len(t) // 2]
+
+
 def e2e_plugins(timed: int = 20, warm: int = 3):
     """GPT-2 small [2, 1024] and BERT-base [8, 512] in f16 (seeded N(0, 0.02) weights): stock
     PyTorch against every op the plug-in swaps (biased Linear, LayerNorm, attention), checked at the
-    north star's 1e-2."""
+    north star's 1e-2. Both forwards are also captured in HIP graphs and timed as replays (these
+    small models are bound by kernel launches), the swapped one checked against its eager output."""
     import torch
     from autokernel_amd import bert, gpt2, verify
     dev = torch.device("cuda:0")
@@ -329,12 +363,28 @@ def e2e_plugins(timed: int = 20, warm: int = 3):
         model = mod.build(torch.float16, dev)
         ids = verify.make_token_ids(model, shape, dev)
         ref_out, ref_ms = verify.benchmark_model(model, ids, warm, timed)
+        graph = {}
+        try:
+            _, graph["torch_graph_ms"] = _graph_timing(lambda: model(ids), timed)
+        except RuntimeError as e:  # recorded, not fatal: the eager figures stand alone
+            graph["torch_graph"] = f"capture failed: {str(e)[:200]}"
         with verify.OptimizedModelContext(model, verify.ALL_KERNELS) as m:
             opt_out, opt_ms = verify.benchmark_model(m, ids, warm, timed)
+            try:
+                g_out, graph["ak_graph_ms"] = _graph_timing(lambda: m(ids), timed)
+                graph["ak_graph_equals_eager"] = bool(torch.equal(g_out, opt_out))
+                del g_out
+            except RuntimeError as e:
+                graph["ak_graph"] = f"capture failed: {str(e)[:200]}"
+        if "torch_graph_ms" in graph and "ak_graph_ms" in graph:
+            graph["graph_speedup"] = round(graph["torch_graph_ms"] / graph["ak_graph_ms"], 3)
+        graph = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in graph.items()}
         cmp = verify.compare_outputs(ref_out, opt_out, torch.float16, 1e-2, 1e-2)
         res.append({"model": name, "input": list(shape), "dtype": "f16", "torch_ms": round(ref_ms, 3),
                     "ak_ms": round(opt_ms, 3), "speedup": round(ref_ms / opt_ms, 3),
-                    "vs_stock_allclose_1e-2": cmp["correctness"], "vs_stock_max_abs": cmp.get("max_abs_error")})
+                    "vs_stock_allclose_1e-2": cmp["correctness"], "vs_stock_max_abs": cmp.get("max_abs_error"),
+                    **graph})
+        log(f"  {name}: eager {ref_ms:.3f} / {opt_ms:.3f} ms; graph {graph}")
         del model, ref_out, opt_out
         torch.cuda.empty_cache()
     return res
